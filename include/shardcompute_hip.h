@@ -1,0 +1,118 @@
+/*
+ * libshardcompute_hip — C-ABI of the MI355X (gfx950) kernels behind ShardCompute's
+ * per-rank quantized inference hot path.
+ *
+ * Conventions for every entry point:
+ *  - Pointers are device pointers (hipMalloc / torch-ROCm tensors), row-major and
+ *    contiguous.  bf16 values are passed as uint16_t bit patterns.
+ *  - Quantized weights use MLX's affine format: uint32 words holding 32/bits codes
+ *    of consecutive columns, least significant first; one bf16 scale and bias per
+ *    group of `group_size` columns; dequantized value = scale * q + bias.
+ *  - Work is enqueued on `hip_stream` (NULL = the null stream) and never
+ *    synchronised; outputs are valid once that stream reaches the work.
+ *  - Return 0 on success, a negative status otherwise (-1 bad argument,
+ *    -2 unsupported configuration, -3 HIP runtime error); sc_last_error() then
+ *    holds a message (thread-local, valid until the next failing call).
+ *  - The kernels allocate nothing per call.  The split-K path of sc_qmm_bf16 uses a
+ *    library-owned scratch per device, allocated on first need and grown (with a
+ *    device synchronisation) when a larger shape arrives: calls that overlap on one
+ *    device (concurrent streams) race on it, and the first call of a new largest
+ *    shape must not happen under stream capture.
+ */
+#ifndef SHARDCOMPUTE_HIP_H
+#define SHARDCOMPUTE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SC_ABI_VERSION 1
+
+/* Kernel selection for sc_qmm_bf16_path. */
+#define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
+#define SC_QMM_PATH_GEMV 1 /* fused dequant-GEMV (decode batches, M <= 32)      */
+#define SC_QMM_PATH_GEMM 2 /* LDS-staged dequant -> bf16 MFMA GEMM (prefill)     */
+
+/* ABI version of the loaded library (SC_ABI_VERSION at build time). */
+int sc_abi_version(void);
+
+/* Message of the last failing call on this thread. */
+const char *sc_last_error(void);
+
+/*
+ * y[M, N] = bf16( x[M, K] @ dequant(wq, scales, biases)^T ), then, when
+ * bias_or_null is given, y = bf16(y + bias[N]).  fp32 accumulation.
+ *   x      bf16 [M, K], 16-byte aligned      wq  uint32 [N, K*bits/32], 16-byte aligned
+ *   scales bf16 [N, K/group_size]            biases bf16 [N, K/group_size]
+ *   bits in {4, 8}, group_size == 64, K % group_size == 0.
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size, bits)
+ * plus the "+ self.bias" that follows it:
+ *   src/shardcompute/parallel/quantized_linear.py:168-180   (QuantizedColumnParallelLinear.forward)
+ *   src/shardcompute/parallel/quantized_linear.py:206-217   (.forward_sync)
+ *   src/shardcompute/parallel/quantized_linear.py:435-443   (QuantizedRowParallelLinear.forward)
+ *   src/shardcompute/parallel/quantized_linear.py:472-480   (.forward_partial)
+ *   src/shardcompute/parallel/transformer.py:639-647, 971-979 (pipeline LinearLayer / lm_head)
+ *   src/shardcompute/model/quantization.py:67-75            (QuantizedWeight.matmul)
+ */
+int sc_qmm_bf16(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                int group_size, void *hip_stream);
+
+/*
+ * sc_qmm_bf16 with an explicit kernel choice (SC_QMM_PATH_*): lets tests and
+ * benchmarks run both kernels on the same shape.  Same reference call sites.
+ */
+int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                     const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                     int group_size, int path, void *hip_stream);
+
+/*
+ * Vocab-sharded bf16 row gather: for t < T,
+ *   out[t, :] = table[ids[t] - vocab_start, :]  if vocab_start <= ids[t] < vocab_start + v_local
+ *             = +0.0                            otherwise,
+ * bit for bit.  ids are int32 (ids_is_int64 = 0) or int64; table bf16 [v_local, D].
+ * Implements the mask/clip/take/where of
+ *   src/shardcompute/parallel/embedding.py:322-356 (QuantizedParallelEmbedding.forward)
+ * on the bf16 table of VocabParallelEmbedding (a stub at embedding.py:397-418), and the
+ * plain lookup mx.take(weight, ids, axis=0) of ParallelEmbedding (embedding.py:131-132,
+ * 164-165) when vocab_start = 0 and v_local = vocab_size.
+ */
+int sc_vocab_gather_bf16(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
+                         int64_t D, int64_t vocab_start, uint16_t *out, void *hip_stream);
+
+/*
+ * Vocab-sharded gather of a quantized table, dequantized to bf16:
+ *   out[t, k] = bf16(scales[r, k/gs] * q[r, k] + biases[r, k/gs]),  r = ids[t] - vocab_start,
+ * for in-shard ids, +0.0 rows otherwise.  wq uint32 [v_local, D*bits/32], D % 64 == 0,
+ * out 16-byte aligned.  Replaces the take + mx.dequantize + where of
+ *   src/shardcompute/parallel/embedding.py:322-356.
+ */
+int sc_qembed_gather_bf16(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq,
+                          const uint16_t *scales, const uint16_t *biases, int64_t v_local, int64_t D,
+                          int64_t vocab_start, int bits, int group_size, uint16_t *out, void *hip_stream);
+
+/*
+ * out[rows, K] = bf16(scales * q + biases) for a whole quantized matrix.  Replaces
+ * mx.dequantize at src/shardcompute/parallel/embedding.py:369-379 and
+ * src/shardcompute/model/quantization.py:44-52.
+ */
+int sc_dequantize_bf16(const uint32_t *wq, const uint16_t *scales, const uint16_t *biases, int64_t rows,
+                       int64_t K, int bits, int group_size, uint16_t *out, void *hip_stream);
+
+/*
+ * MLX affine quantizer on the GPU: fp32 w [rows, K] -> wq uint32 [rows, K*bits/32],
+ * bf16 scales/biases [rows, K/64] (edge-preserving rule, fp32 arithmetic, RNE).
+ * Replaces mx.quantize at src/shardcompute/parallel/quantized_linear.py:116-120, 353-357
+ * and src/shardcompute/parallel/embedding.py:303-307 (followed by a bf16 cast of the
+ * scales and biases).
+ */
+int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int group_size, uint32_t *wq,
+                       uint16_t *scales, uint16_t *biases, void *hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SHARDCOMPUTE_HIP_H */

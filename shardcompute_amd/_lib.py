@@ -1,0 +1,220 @@
+"""ctypes binding of libshardcompute_hip.so over torch-ROCm tensors.
+
+Every wrapper checks shapes/dtypes on the host, allocates its output with torch
+on the input's device, passes raw device pointers and torch's current HIP
+stream, and raises ``RuntimeError`` with the library's message when the C-ABI
+returns a non-zero status.  There is no CPU fallback: if the library is not
+built, or a tensor is not on a GPU, the call raises.
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+from .build import LIB_PATH
+
+ABI_VERSION = 1
+PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+
+# Exported symbols (must match include/shardcompute_hip.h).
+EXPORTS = (
+    "sc_abi_version",
+    "sc_last_error",
+    "sc_qmm_bf16",
+    "sc_qmm_bf16_path",
+    "sc_vocab_gather_bf16",
+    "sc_qembed_gather_bf16",
+    "sc_dequantize_bf16",
+    "sc_quantize_affine",
+)
+
+_lib = None
+_lock = threading.Lock()
+
+# Optional per-launch timing hook used by the benchmark: when set, every qmm
+# launch records a pair of events on the launch stream around the kernel.
+timing_sink = None
+
+
+def load():
+    """Open the library (once).  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m shardcompute_amd.build` "
+                "(there is no CPU fallback for the quantized hot path)")
+        lib = ctypes.CDLL(LIB_PATH)
+        p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        lib.sc_abi_version.argtypes = []
+        lib.sc_abi_version.restype = i32
+        lib.sc_last_error.argtypes = []
+        lib.sc_last_error.restype = ctypes.c_char_p
+        lib.sc_qmm_bf16.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
+        lib.sc_qmm_bf16.restype = i32
+        lib.sc_qmm_bf16_path.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, i32, p]
+        lib.sc_qmm_bf16_path.restype = i32
+        lib.sc_vocab_gather_bf16.argtypes = [p, i32, i64, p, i64, i64, i64, p, p]
+        lib.sc_vocab_gather_bf16.restype = i32
+        lib.sc_qembed_gather_bf16.argtypes = [p, i32, i64, p, p, p, i64, i64, i64, i32, i32, p, p]
+        lib.sc_qembed_gather_bf16.restype = i32
+        lib.sc_dequantize_bf16.argtypes = [p, p, p, i64, i64, i32, i32, p, p]
+        lib.sc_dequantize_bf16.restype = i32
+        lib.sc_quantize_affine.argtypes = [p, i64, i64, i32, i32, p, p, p, p]
+        lib.sc_quantize_affine.restype = i32
+        v = lib.sc_abi_version()
+        if v != ABI_VERSION:
+            raise RuntimeError(f"libshardcompute_hip ABI {v}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def _check(rc, what):
+    if rc != 0:
+        msg = load().sc_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("shardcompute_amd kernels need GPU tensors (no CPU fallback)")
+
+
+def _u32(t):
+    if t.dtype == torch.uint32:
+        return t
+    if t.dtype == torch.int32:
+        return t.view(torch.uint32)
+    raise TypeError(f"packed weights must be uint32 (or int32 bits), got {t.dtype}")
+
+
+def _bf16(t, name):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    return t
+
+
+def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO, out=None):
+    """y = bf16(x @ dequant(wq, scales, biases)^T) (+ bias), x [..., K] -> [..., N]."""
+    lib = load()
+    _require_gpu(x, wq, scales, biases, bias)
+    _bf16(x, "x"), _bf16(scales, "scales"), _bf16(biases, "biases")
+    wq = _u32(wq)
+    if bias is not None:
+        _bf16(bias, "bias")
+        bias = bias.contiguous()
+    lead = x.shape[:-1]
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    M = x2.shape[0]
+    N = wq.shape[0]
+    if wq.dim() != 2 or wq.shape[1] * (32 // bits) != K:
+        raise ValueError(f"packed weight {tuple(wq.shape)} does not match K={K} at {bits} bits")
+    G = K // group_size if group_size else 0
+    if scales.shape != (N, G) or biases.shape != (N, G):
+        raise ValueError(f"scales/biases must be [{N}, {G}], got {tuple(scales.shape)} / {tuple(biases.shape)}")
+    if bias is not None and bias.shape != (N,):
+        raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if M == 0:
+        return y.reshape(*lead, N)
+    wq, scales, biases = wq.contiguous(), scales.contiguous(), biases.contiguous()
+    sink = timing_sink
+    st = _stream(x)
+    if sink is not None:
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+    rc = lib.sc_qmm_bf16_path(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),
+                              M, N, K, bits, group_size, path, st)
+    if sink is not None:
+        ev1.record()
+        sink.append((ev0, ev1, M, N, K, bits))
+    _check(rc, "sc_qmm_bf16")
+    return y.reshape(*lead, N)
+
+
+def vocab_gather(ids, table, vocab_start=0, out=None):
+    """Masked bf16 row gather: ids [...] -> [..., D]; out-of-shard ids give +0 rows."""
+    lib = load()
+    _require_gpu(ids, table)
+    _bf16(table, "table")
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"ids must be int32 or int64, got {ids.dtype}")
+    table = table.contiguous()
+    idc = ids.contiguous()
+    V, D = table.shape
+    res = out if out is not None else torch.empty(tuple(ids.shape) + (D,), dtype=torch.bfloat16,
+                                                  device=table.device)
+    rc = lib.sc_vocab_gather_bf16(_ptr(idc), 1 if idc.dtype == torch.int64 else 0, idc.numel(), _ptr(table),
+                                  V, D, int(vocab_start), _ptr(res), _stream(table))
+    _check(rc, "sc_vocab_gather_bf16")
+    return res
+
+
+def qembed_gather(ids, wq, scales, biases, vocab_start=0, bits=4, group_size=64):
+    """Masked gather + dequantize of a quantized table: ids [...] -> bf16 [..., D]."""
+    lib = load()
+    _require_gpu(ids, wq, scales, biases)
+    wq = _u32(wq).contiguous()
+    _bf16(scales, "scales"), _bf16(biases, "biases")
+    if ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"ids must be int32 or int64, got {ids.dtype}")
+    V = wq.shape[0]
+    D = wq.shape[1] * (32 // bits)
+    idc = ids.contiguous()
+    res = torch.empty(tuple(ids.shape) + (D,), dtype=torch.bfloat16, device=wq.device)
+    rc = lib.sc_qembed_gather_bf16(_ptr(idc), 1 if idc.dtype == torch.int64 else 0, idc.numel(), _ptr(wq),
+                                   _ptr(scales.contiguous()), _ptr(biases.contiguous()), V, D, int(vocab_start),
+                                   bits, group_size, _ptr(res), _stream(wq))
+    _check(rc, "sc_qembed_gather_bf16")
+    return res
+
+
+def dequantize(wq, scales, biases, bits=4, group_size=64):
+    """bf16(scales * q + biases) for a whole packed matrix -> [rows, K]."""
+    lib = load()
+    _require_gpu(wq, scales, biases)
+    wq = _u32(wq).contiguous()
+    rows = wq.shape[0]
+    K = wq.shape[1] * (32 // bits)
+    out = torch.empty((rows, K), dtype=torch.bfloat16, device=wq.device)
+    rc = lib.sc_dequantize_bf16(_ptr(wq), _ptr(_bf16(scales, "scales").contiguous()),
+                                _ptr(_bf16(biases, "biases").contiguous()), rows, K, bits, group_size, _ptr(out),
+                                _stream(wq))
+    _check(rc, "sc_dequantize_bf16")
+    return out
+
+
+def quantize(w, bits=4, group_size=64):
+    """MLX affine quantizer on the GPU: fp32 [rows, K] -> (uint32 wq, bf16 scales, bf16 biases)."""
+    lib = load()
+    _require_gpu(w)
+    if w.dim() != 2:
+        raise ValueError("quantize expects a 2-D weight")
+    w = w.to(torch.float32).contiguous()
+    rows, K = w.shape
+    if bits not in (4, 8):
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    if K % group_size:
+        raise ValueError(f"K={K} must be a multiple of group_size={group_size}")
+    wq = torch.empty((rows, K * bits // 32), dtype=torch.uint32, device=w.device)
+    s = torch.empty((rows, K // group_size), dtype=torch.bfloat16, device=w.device)
+    b = torch.empty_like(s)
+    rc = lib.sc_quantize_affine(_ptr(w), rows, K, bits, group_size, _ptr(wq), _ptr(s), _ptr(b), _stream(w))
+    _check(rc, "sc_quantize_affine")
+    return wq, s, b

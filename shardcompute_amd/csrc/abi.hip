@@ -1,0 +1,210 @@
+// C-ABI of libshardcompute_hip: argument checks, dispatch, error reporting and
+// the library-owned split-K scratch.  Declarations live in
+// include/shardcompute_hip.h, which cites the reference call each entry replaces.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "sc_common.h"
+#include "../../include/shardcompute_hip.h"
+
+namespace sc {
+
+int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                        const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+int launch_vocab_gather(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
+                        int64_t D, int64_t vocab_start, uint16_t *out, hipStream_t stream);
+int launch_qembed_gather(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq, const uint16_t *s,
+                         const uint16_t *b, int64_t v_local, int64_t D, int64_t vocab_start, int bits,
+                         uint16_t *out, hipStream_t stream);
+int launch_quantize(const float *w, int64_t rows, int64_t K, int bits, uint32_t *wq, uint16_t *s, uint16_t *b,
+                    hipStream_t stream);
+int launch_dequantize(const uint32_t *wq, const uint16_t *s, const uint16_t *b, int64_t rows, int64_t K, int bits,
+                      uint16_t *out, hipStream_t stream);
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_mu;
+static DeviceInfo g_info[kMaxDevices];
+static bool g_info_ok[kMaxDevices];
+
+struct ScratchSlot {
+    float *partials = nullptr;
+    unsigned *counters = nullptr;
+    size_t partial_cap = 0;
+    size_t counter_cap = 0;
+};
+static ScratchSlot g_scratch[kMaxDevices];
+
+const DeviceInfo &device_info() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
+    if (!g_info_ok[dev]) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_info_ok[dev]) {
+            DeviceInfo di;
+            int v = 0;
+            di.num_cus = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess ? v : 256;
+            di.max_lds_per_block =
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess ? v : 65536;
+            g_info[dev] = di;
+            g_info_ok[dev] = true;
+        }
+    }
+    return g_info[dev];
+}
+
+// Grows (never shrinks) the calling device's split-K scratch.  Counters must
+// start at zero; the kernels return every counter they use to zero.  Growing
+// synchronises the device so no in-flight kernel still uses the old buffers.
+int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out) {
+    int dev = 0;
+    SC_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(SC_EINVAL, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_mu);
+    ScratchSlot &sl = g_scratch[dev];
+    if (sl.partial_cap < partial_floats || sl.counter_cap < n_counters) {
+        const size_t pc = partial_floats > sl.partial_cap ? partial_floats : sl.partial_cap;
+        const size_t cc = n_counters > sl.counter_cap ? n_counters : sl.counter_cap;
+        SC_HIP_CHECK(hipDeviceSynchronize());
+        if (sl.partials) SC_HIP_CHECK(hipFree(sl.partials));
+        if (sl.counters) SC_HIP_CHECK(hipFree(sl.counters));
+        sl.partials = nullptr;
+        sl.counters = nullptr;
+        sl.partial_cap = sl.counter_cap = 0;
+        SC_HIP_CHECK(hipMalloc(&sl.partials, pc * sizeof(float)));
+        SC_HIP_CHECK(hipMalloc(&sl.counters, cc * sizeof(unsigned)));
+        SC_HIP_CHECK(hipMemset(sl.counters, 0, cc * sizeof(unsigned)));
+        SC_HIP_CHECK(hipDeviceSynchronize());
+        sl.partial_cap = pc;
+        sl.counter_cap = cc;
+    }
+    out->partials = sl.partials;
+    out->counters = sl.counters;
+    return SC_OK;
+}
+
+static bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+static int check_qmm(const void *x, const void *wq, const void *s, const void *b, const void *y, int64_t M,
+                     int64_t N, int64_t K, int bits, int group_size) {
+    if (!x || !wq || !s || !b || !y) return set_error(SC_EINVAL, "qmm: null pointer argument");
+    if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "qmm: bits=%d (supported: 4, 8)", bits);
+    if (group_size != 64) return set_error(SC_EUNSUPPORTED, "qmm: group_size=%d (supported: 64)", group_size);
+    if (M < 1 || N < 1 || K < 1) return set_error(SC_EINVAL, "qmm: empty shape M=%lld N=%lld K=%lld",
+                                                  (long long)M, (long long)N, (long long)K);
+    if (K % group_size) return set_error(SC_EINVAL, "qmm: K=%lld not a multiple of group_size=%d", (long long)K,
+                                         group_size);
+    if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+        return set_error(SC_EINVAL, "qmm: dimension above 2^30");
+    if (!aligned(x, 16) || !aligned(wq, 16))
+        return set_error(SC_EINVAL, "qmm: x and wq must be 16-byte aligned");
+    if (!aligned(s, 2) || !aligned(b, 2) || !aligned(y, 2))
+        return set_error(SC_EINVAL, "qmm: scales, biases and y must be 2-byte aligned");
+    return SC_OK;
+}
+
+static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                        const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                        int group_size, void *stream, int path) {
+    int rc = check_qmm(x, wq, s, b, y, M, N, K, bits, group_size);
+    if (rc) return rc;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (path == SC_QMM_PATH_AUTO) path = (M <= 32) ? SC_QMM_PATH_GEMV : SC_QMM_PATH_GEMM;
+    if (path == SC_QMM_PATH_GEMV) {
+        rc = launch_qgemv_skinny(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        // x rows that do not fit LDS for the skinny kernel go to the tiled GEMM
+        if (rc == SC_EUNSUPPORTED && M > 1)
+            return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        return rc;
+    }
+    if (path == SC_QMM_PATH_GEMM) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+    return set_error(SC_EINVAL, "qmm: unknown path %d", path);
+}
+
+}  // namespace sc
+
+using namespace sc;
+
+extern "C" {
+
+int sc_abi_version(void) { return SC_ABI_VERSION; }
+
+const char *sc_last_error(void) { return g_err; }
+
+int sc_qmm_bf16(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                int group_size, void *hip_stream) {
+    return qmm_dispatch(x, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream,
+                        SC_QMM_PATH_AUTO);
+}
+
+int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                     const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                     int group_size, int path, void *hip_stream) {
+    return qmm_dispatch(x, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream, path);
+}
+
+int sc_vocab_gather_bf16(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
+                         int64_t D, int64_t vocab_start, uint16_t *out, void *hip_stream) {
+    if (T < 0 || v_local < 1 || D < 1) return set_error(SC_EINVAL, "vocab_gather: T=%lld v_local=%lld D=%lld",
+                                                        (long long)T, (long long)v_local, (long long)D);
+    if (T == 0) return SC_OK;
+    if (!ids || !table || !out) return set_error(SC_EINVAL, "vocab_gather: null pointer argument");
+    if (!aligned(ids, ids_is_int64 ? 8 : 4) || !aligned(table, 2) || !aligned(out, 2))
+        return set_error(SC_EINVAL, "vocab_gather: misaligned pointer");
+    return launch_vocab_gather(ids, ids_is_int64, T, table, v_local, D, vocab_start, out,
+                               reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_qembed_gather_bf16(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq,
+                          const uint16_t *scales, const uint16_t *biases, int64_t v_local, int64_t D,
+                          int64_t vocab_start, int bits, int group_size, uint16_t *out, void *hip_stream) {
+    if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "qembed_gather: bits=%d", bits);
+    if (group_size != 64) return set_error(SC_EUNSUPPORTED, "qembed_gather: group_size=%d", group_size);
+    if (T < 0 || v_local < 1 || D < 1 || D % 64)
+        return set_error(SC_EINVAL, "qembed_gather: T=%lld v_local=%lld D=%lld (D must be a multiple of 64)",
+                         (long long)T, (long long)v_local, (long long)D);
+    if (T == 0) return SC_OK;
+    if (!ids || !wq || !scales || !biases || !out) return set_error(SC_EINVAL, "qembed_gather: null pointer");
+    if (!aligned(out, 16) || !aligned(wq, 4)) return set_error(SC_EINVAL, "qembed_gather: misaligned pointer");
+    return launch_qembed_gather(ids, ids_is_int64, T, wq, scales, biases, v_local, D, vocab_start, bits, out,
+                                reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_dequantize_bf16(const uint32_t *wq, const uint16_t *scales, const uint16_t *biases, int64_t rows,
+                       int64_t K, int bits, int group_size, uint16_t *out, void *hip_stream) {
+    if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "dequantize: bits=%d", bits);
+    if (group_size != 64) return set_error(SC_EUNSUPPORTED, "dequantize: group_size=%d", group_size);
+    if (rows < 0 || K < 1 || K % 64) return set_error(SC_EINVAL, "dequantize: rows=%lld K=%lld", (long long)rows,
+                                                      (long long)K);
+    if (rows == 0) return SC_OK;
+    if (!wq || !scales || !biases || !out) return set_error(SC_EINVAL, "dequantize: null pointer");
+    return launch_dequantize(wq, scales, biases, rows, K, bits, out, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int group_size, uint32_t *wq,
+                       uint16_t *scales, uint16_t *biases, void *hip_stream) {
+    if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "quantize: bits=%d", bits);
+    if (group_size != 64) return set_error(SC_EUNSUPPORTED, "quantize: group_size=%d", group_size);
+    if (rows < 0 || K < 1 || K % 64) return set_error(SC_EINVAL, "quantize: rows=%lld K=%lld", (long long)rows,
+                                                      (long long)K);
+    if (rows == 0) return SC_OK;
+    if (!w || !wq || !scales || !biases) return set_error(SC_EINVAL, "quantize: null pointer");
+    return launch_quantize(w, rows, K, bits, wq, scales, biases, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+}  // extern "C"

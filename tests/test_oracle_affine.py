@@ -1,0 +1,265 @@
+"""Pins oracle/mlx_affine.py (format, dequantize, quantized matmul, quantizer).
+
+No golden vectors for this path exist in the reference and MLX is not
+importable, so each oracle function is pinned by known answers, closed forms,
+an independent implementation and the reference tests' shard invariants
+(``tests/test_parallel_layers.py:55-138``), chosen so that a dropped term, a
+swapped nibble order or a transposed operand fails at least one of them.
+"""
+import numpy as np
+import pytest
+
+from oracle import cref
+from oracle.bf16 import bf16_to_f32, f32_to_bf16
+from oracle.mlx_affine import (dequantize_bf16, dequantize_f64, pack, quantize, quantize_bf16,
+                               quantized_matmul_bf16, quantized_matmul_f64, unpack)
+
+
+# ---------------------------------------------------------------- format
+
+def test_pack_known_answer_w4():
+    q = np.array([[0, 1, 2, 3, 4, 5, 6, 7, 15, 14, 13, 12, 11, 10, 9, 8]], np.uint32)
+    assert pack(q, 4).tolist() == [[0x76543210, 0x89ABCDEF]]
+
+
+def test_pack_known_answer_w8():
+    q = np.array([[1, 2, 3, 4, 255, 0, 128, 7]], np.uint32)
+    assert pack(q, 8).tolist() == [[0x04030201, 0x078000FF]]
+
+
+def _unpack_bitstring(wq, bits):
+    """Independent unpacker: read each word as a binary string, LSB field first."""
+    out = []
+    for row in np.asarray(wq, np.uint32):
+        vals = []
+        for word in row:
+            s = format(int(word), "032b")
+            fields = [s[32 - (j + 1) * bits: 32 - j * bits] for j in range(32 // bits)]
+            vals.extend(int(f, 2) for f in fields)
+        out.append(vals)
+    return np.array(out, np.uint8)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_unpack_matches_bitstring_and_roundtrips(bits):
+    rng = np.random.default_rng(bits)
+    q = rng.integers(0, 1 << bits, size=(5, 64), dtype=np.uint32)
+    wq = pack(q, bits)
+    assert wq.shape == (5, 64 * bits // 32)
+    assert np.array_equal(unpack(wq, bits), q.astype(np.uint8))
+    assert np.array_equal(_unpack_bitstring(wq, bits), q.astype(np.uint8))
+
+
+# ---------------------------------------------------------------- dequantize
+
+def test_dequantize_closed_forms():
+    rng = np.random.default_rng(1)
+    q = rng.integers(0, 16, size=(3, 128), dtype=np.uint32)
+    wq = pack(q, 4)
+    one = f32_to_bf16(np.ones((3, 2), np.float32))
+    zero = f32_to_bf16(np.zeros((3, 2), np.float32))
+    assert np.array_equal(dequantize_f64(wq, one, zero, 64, 4), q.astype(np.float64))
+    b = f32_to_bf16(rng.standard_normal((3, 2)).astype(np.float32))
+    w = dequantize_f64(wq, zero, b, 64, 4)
+    assert np.array_equal(w, np.repeat(bf16_to_f32(b).astype(np.float64), 64, axis=1))
+    # group boundaries: group g covers columns [64g, 64g + 64)
+    s = f32_to_bf16(np.array([[1.0, 2.0]] * 3, np.float32))
+    w = dequantize_f64(wq, s, zero, 64, 4)
+    assert np.array_equal(w[:, :64], q[:, :64]) and np.array_equal(w[:, 64:], 2 * q[:, 64:])
+
+
+def test_dequantize_bf16_definition():
+    rng = np.random.default_rng(2)
+    w = rng.standard_normal((4, 256)).astype(np.float32) * 0.05
+    wq, s, b = quantize_bf16(w, 64, 4)
+    got = dequantize_bf16(wq, s, b, 64, 4)
+    exact = dequantize_f64(wq, s, b, 64, 4)
+    # one rounding of the (fp32-exact) value: within half a bf16 ulp of the exact value
+    g = bf16_to_f32(got).astype(np.float64)
+    _, e = np.frexp(exact)
+    half_ulp = np.ldexp(1.0, e - 9)  # bf16 keeps 8 significant bits
+    assert np.all(np.abs(g - exact) <= half_ulp)
+
+
+# ---------------------------------------------------------------- quantized matmul
+
+def _brute_qmm(x, wq, s, b, bits, gs):
+    """Scalar triple loop straight from the definition (tiny sizes only)."""
+    xf = bf16_to_f32(x).astype(np.float64)
+    sf = bf16_to_f32(s).astype(np.float64)
+    bf = bf16_to_f32(b).astype(np.float64)
+    pf = 32 // bits
+    M, K = xf.shape
+    N = wq.shape[0]
+    y = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                word = int(wq[n, k // pf])
+                q = (word >> ((k % pf) * bits)) & ((1 << bits) - 1)
+                acc += xf[m, k] * (sf[n, k // gs] * q + bf[n, k // gs])
+            y[m, n] = acc
+    return y
+
+
+def _rand_case(rng, M, K, N, bits, gs=64):
+    x = f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    wq, s, b = quantize_bf16(w, gs, bits)
+    return x, wq, s, b
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_matches_bruteforce(bits):
+    rng = np.random.default_rng(3)
+    x, wq, s, b = _rand_case(rng, 3, 128, 5, bits)
+    assert np.allclose(quantized_matmul_f64(x, wq, s, b, 64, bits),
+                       _brute_qmm(x, wq, s, b, bits, 64), rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_onehot_selects_columns():
+    rng = np.random.default_rng(4)
+    M, K, N = 4, 256, 32
+    x = f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    cols = rng.integers(0, K, size=N)
+    q = np.zeros((N, K), np.uint32)
+    q[np.arange(N), cols] = 1
+    one = f32_to_bf16(np.ones((N, K // 64), np.float32))
+    zero = np.zeros((N, K // 64), np.uint16)
+    y = quantized_matmul_f64(x, pack(q, 4), one, zero, 64, 4)
+    assert np.array_equal(y, bf16_to_f32(x)[:, cols].astype(np.float64))
+
+
+def test_qmm_zero_scale_gives_bias_weighted_group_sums():
+    rng = np.random.default_rng(5)
+    M, K, N = 2, 192, 7
+    x, wq, _, b = _rand_case(rng, M, K, N, 4)
+    zero = np.zeros_like(b)
+    y = quantized_matmul_f64(x, wq, zero, b, 64, 4)
+    xs = bf16_to_f32(x).astype(np.float64).reshape(M, K // 64, 64).sum(-1)
+    assert np.allclose(y, xs @ bf16_to_f32(b).astype(np.float64).T, rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_non_square_transpose_orientation():
+    # y must be [M, N] with W stored [N, K]; a transposed operand cannot even run
+    rng = np.random.default_rng(6)
+    x, wq, s, b = _rand_case(rng, 2, 320, 48, 4)
+    y = quantized_matmul_f64(x, wq, s, b, 64, 4)
+    assert y.shape == (2, 48)
+    w = dequantize_f64(wq, s, b, 64, 4)
+    assert np.allclose(y, bf16_to_f32(x).astype(np.float64) @ w.T)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_column_shards_concat_to_full(bits):
+    """Restates tests/test_parallel_layers.py:55-85 for the quantized layer."""
+    rng = np.random.default_rng(7)
+    x, wq, s, b = _rand_case(rng, 3, 256, 64, bits)
+    full = quantized_matmul_f64(x, wq, s, b, 64, bits)
+    parts = [quantized_matmul_f64(x, wq[r * 32:(r + 1) * 32], s[r * 32:(r + 1) * 32],
+                                  b[r * 32:(r + 1) * 32], 64, bits) for r in range(2)]
+    assert np.array_equal(np.concatenate(parts, axis=1), full)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qmm_row_shards_sum_to_full(bits):
+    """Restates tests/test_parallel_layers.py:103-138: row partials sum to the full output."""
+    rng = np.random.default_rng(8)
+    K = 512
+    x, wq, s, b = _rand_case(rng, 2, K, 16, bits)
+    full = quantized_matmul_f64(x, wq, s, b, 64, bits)
+    wpr = wq.shape[1] // 2
+    gpr = s.shape[1] // 2
+    xs = [x[:, :K // 2], x[:, K // 2:]]
+    parts = [quantized_matmul_f64(xs[r], wq[:, r * wpr:(r + 1) * wpr], s[:, r * gpr:(r + 1) * gpr],
+                                  b[:, r * gpr:(r + 1) * gpr], 64, bits) for r in range(2)]
+    assert np.allclose(parts[0] + parts[1], full, rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_linear_in_x():
+    rng = np.random.default_rng(9)
+    x1, wq, s, b = _rand_case(rng, 2, 128, 8, 4)
+    x2 = f32_to_bf16(rng.standard_normal((2, 128)).astype(np.float32))
+    f = lambda x: quantized_matmul_f64(x, wq, s, b, 64, 4)
+    xsum = bf16_to_f32(x1).astype(np.float64) + bf16_to_f32(x2).astype(np.float64)
+    assert np.allclose(f(xsum), f(x1) + f(x2), rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_bf16_bias_is_added_after_rounding():
+    rng = np.random.default_rng(10)
+    x, wq, s, b = _rand_case(rng, 2, 128, 8, 4)
+    bias = f32_to_bf16(rng.standard_normal(8).astype(np.float32))
+    y0 = quantized_matmul_bf16(x, wq, s, b, None, 64, 4)
+    y1 = quantized_matmul_bf16(x, wq, s, b, bias, 64, 4)
+    assert np.array_equal(y1, f32_to_bf16(bf16_to_f32(y0) + bf16_to_f32(bias)[None]))
+
+
+# ---------------------------------------------------------------- C restatement
+
+@pytest.fixture(scope="module")
+def clib():
+    if not cref.available():
+        cref.build()
+    return cref.load()
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M", [1, 5])
+def test_c_restatement_matches_numpy(clib, bits, M):
+    rng = np.random.default_rng(11 + bits + M)
+    x, wq, s, b = _rand_case(rng, M, 1024, 96, bits)
+    bias = f32_to_bf16(rng.standard_normal(96).astype(np.float32))
+    for bb in (None, bias):
+        yc = cref.qmm_bf16(x, wq, s, b, bb, 64, bits, threads=4)
+        yn = quantized_matmul_bf16(x, wq, s, b, bb, 64, bits)
+        d = np.abs(yc.astype(np.int32) - yn.astype(np.int32))
+        # both accumulate in double (different order); outputs agree to the bf16 bit,
+        # except a rare neighbour when an fp64 sum sits on a rounding boundary
+        assert d.max() <= 1 and (d > 0).mean() < 1e-3
+
+
+# ---------------------------------------------------------------- quantizer
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantizer_properties(bits):
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((16, 512)) * 0.02).astype(np.float32)
+    w[0, :64] = 0.37  # constant group
+    w[1, :64] = 0.0   # all-zero group
+    wq, s, b = quantize(w, 64, bits)
+    q = unpack(wq, bits).astype(np.float64)
+    assert q.max() <= (1 << bits) - 1
+    S = np.repeat(s, 64, 1).astype(np.float64)
+    B = np.repeat(b, 64, 1).astype(np.float64)
+    deq = S * q + B
+    # values inside the representable range [b, b + n_bins*s] land within half a step;
+    # the refit scale (edge / round(edge / scale)) can shrink the range, so the far end
+    # may clip, by less than one original step
+    lo = np.minimum(B, B + S * ((1 << bits) - 1))
+    hi = np.maximum(B, B + S * ((1 << bits) - 1))
+    inside = (w >= lo) & (w <= hi)
+    err = np.abs(deq - w)
+    assert np.all(err[inside] <= np.abs(S[inside]) / 2 * (1 + 1e-5) + 1e-9)
+    assert np.all(err <= 1.5 * np.abs(S) + 1e-9)
+    assert inside.mean() > 0.95
+    # the larger-magnitude end of each group is reproduced exactly (bias = edge, q = 0)
+    g = w.reshape(16, -1, 64)
+    edge = np.where(np.abs(g.min(-1)) > np.abs(g.max(-1)), g.min(-1), g.max(-1))
+    nz = edge != 0
+    assert np.array_equal(b[nz], edge[nz])
+    assert np.all(deq.reshape(16, -1, 64)[:, 0, :][0] == np.float32(0.37))
+    assert np.all(deq[1, :64] == 0.0)
+    # codes are monotone in w within a group
+    order = np.argsort(g, axis=-1)
+    qs = np.take_along_axis(q.reshape(16, -1, 64), order, -1)
+    sign = np.sign(s)[..., None]
+    assert np.all(np.diff(qs, axis=-1) * sign >= 0)
+
+
+def test_quantizer_rejects_bad_params():
+    w = np.zeros((2, 128), np.float32)
+    with pytest.raises(ValueError):
+        quantize(w, 64, 3)
+    with pytest.raises(ValueError):
+        quantize(np.zeros((2, 100), np.float32), 64, 4)
