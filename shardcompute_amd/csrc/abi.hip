@@ -12,6 +12,10 @@
 
 namespace sc {
 
+int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                        const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -125,11 +129,16 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (path == SC_QMM_PATH_AUTO) path = (M <= 32) ? SC_QMM_PATH_GEMV : SC_QMM_PATH_GEMM;
     if (path == SC_QMM_PATH_GEMV) {
+        // M <= 8: persistent LDS-DMA GEMV; otherwise (or when x does not fit its
+        // LDS) the 16-column split-K GEMV; K not a multiple of 512 (W4) / 256 (W8)
+        // takes the 32-column generic-K kernel; x that fits no LDS layout, the GEMM
+        rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        if (rc != SC_EUNSUPPORTED) return rc;
+        rc = launch_qgemv16(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        if (rc != SC_EUNSUPPORTED) return rc;
         rc = launch_qgemv_skinny(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
-        // x rows that do not fit LDS for the skinny kernel go to the tiled GEMM
-        if (rc == SC_EUNSUPPORTED && M > 1)
-            return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
-        return rc;
+        if (rc != SC_EUNSUPPORTED) return rc;
+        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
     }
     if (path == SC_QMM_PATH_GEMM) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
     return set_error(SC_EINVAL, "qmm: unknown path %d", path);

@@ -1,4 +1,5 @@
-// Kernel A: fused dequant-GEMV for decode-sized batches (M <= 32 rows of x).
+// Kernel A, generic-K variant: fused dequant-GEMV for M <= 32 rows of x when K is
+// a multiple of 64 but not of the 512 (W4) / 256 (W8) that qgemv16.hip needs.
 //
 // Computes y[m, n] = sum_k x[m, k] * (s[n, g] * q[n, k] + b[n, g]),  g = k / 64,
 // for MLX-affine 4/8-bit weights stored [N, K*bits/32] uint32 with bf16 s, b
@@ -21,9 +22,8 @@
 //   the W4 slot order; rows >= M read row M-1 and their outputs are dropped.
 // * No dequantized weight ever reaches memory: HBM traffic is the packed
 //   weights, scales, biases, x and y.
-// * Waves reduce through LDS; with split-K, the partial tiles go to a
-//   library-owned fp32 scratch and the last-arriving workgroup of a tile sums
-//   them in split order (deterministic) and writes bf16.
+// * Waves of the workgroup split K and reduce through LDS; one workgroup covers
+//   all of K for its tile (the staged x must fit LDS).
 #include "sc_common.h"
 
 namespace sc {
@@ -35,8 +35,6 @@ struct SkinnyArgs {
     const uint16_t *b;
     const uint16_t *bias;
     uint16_t *y;
-    float *partials;      // [splits, M, N] (split-K only)
-    unsigned *counters;   // [n_tiles]      (split-K only)
     int M, N, K, G;
     int groups_per_split;
     int vec_sb;           // scales/biases rows are 16-byte aligned and G % 8 == 0
@@ -73,7 +71,6 @@ __global__ void __launch_bounds__(64 * kMaxWaves) qgemv_skinny_kernel(SkinnyArgs
     // the MFMAs) only where the register budget allows it without spills.
     constexpr bool PREFETCH = (BITS == 4 && NREG <= 4);
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ int s_is_last;
     constexpr int U4_PER_GROUP_HALF = BITS / 4;     // uint4 loads per lane per group
     constexpr int U4_PER_GROUP_ROW = BITS / 2;      // uint4 per group in a row
 
@@ -82,8 +79,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) qgemv_skinny_kernel(SkinnyArgs
     const int wave = tid >> 6;
     const int nwaves = blockDim.x >> 6;
     const int tile = blockIdx.x;
-    const int split = blockIdx.y;
-    const int nsplit = gridDim.y;
+    const int split = 0;
     const int M = a.M, N = a.N;
 
     const int g_begin = split * a.groups_per_split;
@@ -228,40 +224,11 @@ __global__ void __launch_bounds__(64 * kMaxWaves) qgemv_skinny_kernel(SkinnyArgs
         const int row = dout_row(r, l >> 5);
         const int nn = tile * 32 + (l & 31);
         if (row < M && nn < N) {
-            if (nsplit == 1) {
-                uint32_t o = f2bf(v);
-                if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
-                a.y[(size_t)row * N + nn] = (uint16_t)o;
-            } else {
-                a.partials[((size_t)split * M + row) * N + nn] = v;
-            }
+            uint32_t o = f2bf(v);
+            if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
+            a.y[(size_t)row * N + nn] = (uint16_t)o;
         }
     }
-    if (nsplit == 1) return;
-
-    // ---- split-K: the last workgroup of this tile to arrive sums the partials
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = atomicAdd(&a.counters[tile], 1u);
-        s_is_last = (prev == (unsigned)(nsplit - 1));
-    }
-    __syncthreads();
-    if (!s_is_last) return;
-    __threadfence();
-    for (int idx = tid; idx < M * 32; idx += blockDim.x) {
-        const int row = idx >> 5;
-        const int nn = tile * 32 + (idx & 31);
-        if (nn >= N) continue;
-        float v = 0.f;
-        for (int sp = 0; sp < nsplit; ++sp)
-            v += __hip_atomic_load(&a.partials[((size_t)sp * M + row) * N + nn], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t o = f2bf(v);
-        if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
-        a.y[(size_t)row * N + nn] = (uint16_t)o;
-    }
-    if (tid == 0) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- host launch
@@ -278,31 +245,20 @@ static int lds_need(int M, int gps, int waves, int nreg) {
 
 static int nreg_for(int M) { return M == 1 ? 1 : M <= 8 ? 4 : M <= 16 ? 8 : 16; }
 
-// Chooses split-K and waves per workgroup: enough workgroups for every CU,
-// at least one 8-group chunk per wave, and the staged x within LDS.
+// Waves per workgroup: at least one 8-group chunk per wave; the staged x must fit LDS.
 static bool plan_skinny(int M, int N, int G, SkinnyPlan *p) {
     const DeviceInfo &di = device_info();
-    const int tiles = (N + 31) / 32;
+    (void)N;
     const int nreg = nreg_for(M);
-    int splits = 1;
-    while (tiles * splits < di.num_cus && (G + splits * 2 - 1) / (splits * 2) >= 8) splits *= 2;
-    for (;;) {
-        int gps = (G + splits - 1) / splits;
-        if (splits > 1) gps = (gps + 7) & ~7;
-        const int real_splits = (G + gps - 1) / gps;
-        const int chunks = (gps + 7) / 8;
-        const int waves = chunks < kMaxWaves ? chunks : kMaxWaves;
-        const int lds = lds_need(M, gps, waves, nreg);
-        if (lds <= di.max_lds_per_block) {
-            p->splits = real_splits;
-            p->groups_per_split = gps;
-            p->waves = waves;
-            p->lds_bytes = lds;
-            return true;
-        }
-        if (gps <= 8) return false;
-        splits *= 2;
-    }
+    const int chunks = (G + 7) / 8;
+    const int waves = chunks < kMaxWaves ? chunks : kMaxWaves;
+    const int lds = lds_need(M, G, waves, nreg);
+    if (lds > di.max_lds_per_block) return false;
+    p->splits = 1;
+    p->groups_per_split = G;
+    p->waves = waves;
+    p->lds_bytes = lds;
+    return true;
 }
 
 template <int BITS, int NREG>
@@ -330,17 +286,9 @@ int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         return set_error(SC_EUNSUPPORTED, "qgemv: x tile of M=%d K=%d does not fit LDS", M, K);
     SkinnyArgs a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
-    a.partials = nullptr; a.counters = nullptr;
     a.M = M; a.N = N; a.K = K; a.G = G;
     a.groups_per_split = p.groups_per_split;
     a.vec_sb = ((G % 8) == 0 && ((uintptr_t)s % 16) == 0 && ((uintptr_t)b % 16) == 0) ? 1 : 0;
-    if (p.splits > 1) {
-        SplitKScratch ws;
-        const int rc = splitk_scratch((size_t)p.splits * M * N, (size_t)(N + 31) / 32, &ws);
-        if (rc) return rc;
-        a.partials = ws.partials;
-        a.counters = ws.counters;
-    }
     const int nreg = nreg_for(M);
 #define SC_SKINNY(BITS_, NREG_) \
     if (bits == BITS_ && nreg == NREG_) return launch_skinny_t<BITS_, NREG_>(a, p, stream);

