@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 1
+#define SC_ABI_VERSION 2
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -110,6 +110,90 @@ int sc_dequantize_bf16(const uint32_t *wq, const uint16_t *scales, const uint16_
  */
 int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int group_size, uint32_t *wq,
                        uint16_t *scales, uint16_t *biases, void *hip_stream);
+
+/* ------------------------------------------------------------------------------
+ * Decoder wiring around the quantized linears.  The cache length (the number of
+ * positions already in the KV cache) is read from device memory, so a decode step
+ * captured once in a HIP graph replays at every position.
+ *
+ * KV cache per layer, capacity T_cap (a multiple of 32), zero-initialised:
+ *   k_cache   [B, Hkv, T_cap, D] bf16
+ *   v_cache_t [B, Hkv, D, T_cap] bf16 (values transposed)
+ * ---------------------------------------------------------------------------- */
+
+/*
+ * h = x + residual (bf16, when residual_or_null is given; written to h_out_or_null
+ * when that is given) and y = (h / sqrt(mean(h*h) + eps)) * weight, row-wise over
+ * D (a multiple of 8, at most 16384).  Replaces RMSNorm.__call__ at
+ * src/shardcompute/parallel/transformer.py:46-61 and the residual adds of
+ * ParallelTransformerBlock.forward at transformer.py:246 and :252.
+ */
+int sc_rms_norm_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *weight, uint16_t *y,
+                     uint16_t *h_out_or_null, int64_t rows, int64_t D, float eps, void *hip_stream);
+
+/*
+ * RoPE on the q and k heads of the fused projection rows qkv [B*S, qkv_stride]
+ * (q heads, then k heads, then v heads, each D wide).  Token s of each sequence
+ * goes to cache slot cache_len[0] + s and is rotated for position
+ * cache_len[0] + s + pos_offset (rotate-half, fp32 tables cos_t/sin_t
+ * [table_len, D/2]); rotated q is written back in place, rotated k and v are
+ * appended to the cache.  Replaces RoPE.__call__ / RoPE._rotate and the KV
+ * concatenation of ParallelAttention.forward at
+ * src/shardcompute/parallel/attention.py:94-151 and :421-435.
+ */
+int sc_rope_append_kv_bf16(uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t S, int64_t H, int64_t Hkv,
+                           int64_t D, const float *cos_t, const float *sin_t, int64_t table_len, uint16_t *k_cache,
+                           uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len, int64_t pos_offset,
+                           void *hip_stream);
+
+/* Bytes of workspace sc_attention_bf16 needs for these sizes (0: none). */
+int64_t sc_attention_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap);
+
+/*
+ * Causal GQA attention of S new positions per sequence against the cache, which
+ * holds cache_len[0] earlier positions followed by the S new ones (appended by
+ * sc_rope_append_kv_bf16 with the same cache_len): out = softmax(q k^T * scale +
+ * causal mask) v, q head h reading KV head h / (H / Hkv).  q rows at
+ * q + (b*S + s)*q_stride + h*D, output rows likewise with out_stride.  D is 64 or
+ * 128.  Replaces the score / mask / softmax / value steps of
+ * ParallelAttention.forward at src/shardcompute/parallel/attention.py:437-466.
+ */
+int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache, const uint16_t *v_cache_t,
+                      int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, void *workspace,
+                      int64_t workspace_bytes, void *hip_stream);
+
+/*
+ * out[rows, I] = silu(gate) * up for gate_up [rows, 2I] (gate columns first), with
+ * silu(g) = g / (1 + exp(-g)).  Replaces the activation step of ParallelMLP.forward
+ * at src/shardcompute/parallel/mlp.py:161-162 and :241-245.
+ */
+int sc_silu_mul_bf16(const uint16_t *gate_up, int64_t rows, int64_t I, uint16_t *out, void *hip_stream);
+
+/*
+ * ids[r] = first index of the maximum of logits row r (NaN counts as the maximum,
+ * -0.0 equals +0.0).  When tokens_or_null is given the id is also stored at
+ * tokens[r*tokens_stride + c] with c = (step_or_null ? step[0] : 0), provided
+ * 0 <= c < tokens_cols (otherwise only ids is written).  Replaces the greedy
+ * mx.argmax of ParallelExecutor.generate at src/shardcompute/worker/executor.py:276-278.
+ */
+int sc_argmax_bf16(const uint16_t *logits, int64_t rows, int64_t V, int32_t *ids, int32_t *tokens_or_null,
+                   int64_t tokens_stride, int64_t tokens_cols, const int32_t *step_or_null, void *hip_stream);
+
+/*
+ * out = a + b elementwise in bf16 (n a multiple of 8): the residual adds of
+ * ParallelTransformerBlock.forward at src/shardcompute/parallel/transformer.py:246, :252
+ * where no normalisation follows.
+ */
+int sc_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n, void *hip_stream);
+
+/*
+ * counters[i] += delta for i < n (n <= 64), on the stream: advances the device-side
+ * cache length / step counters between graph replays.  Stands in for the
+ * cache-length bookkeeping of src/shardcompute/worker/executor.py:134-136 (the cache
+ * grows by the step's sequence length).
+ */
+int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream);
 
 #ifdef __cplusplus
 }

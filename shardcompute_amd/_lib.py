@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -27,6 +27,14 @@ EXPORTS = (
     "sc_qembed_gather_bf16",
     "sc_dequantize_bf16",
     "sc_quantize_affine",
+    "sc_rms_norm_bf16",
+    "sc_rope_append_kv_bf16",
+    "sc_attention_workspace_bytes",
+    "sc_attention_bf16",
+    "sc_silu_mul_bf16",
+    "sc_argmax_bf16",
+    "sc_add_bf16",
+    "sc_add_i32",
 )
 
 _lib = None
@@ -67,6 +75,23 @@ def load():
         lib.sc_dequantize_bf16.restype = i32
         lib.sc_quantize_affine.argtypes = [p, i64, i64, i32, i32, p, p, p, p]
         lib.sc_quantize_affine.restype = i32
+        f32 = ctypes.c_float
+        lib.sc_rms_norm_bf16.argtypes = [p, p, p, p, p, i64, i64, f32, p]
+        lib.sc_rms_norm_bf16.restype = i32
+        lib.sc_rope_append_kv_bf16.argtypes = [p, i64, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, p]
+        lib.sc_rope_append_kv_bf16.restype = i32
+        lib.sc_attention_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64]
+        lib.sc_attention_workspace_bytes.restype = i64
+        lib.sc_attention_bf16.argtypes = [p, i64, p, p, i64, p, p, i64, i64, i64, i64, i64, i64, f32, p, i64, p]
+        lib.sc_attention_bf16.restype = i32
+        lib.sc_silu_mul_bf16.argtypes = [p, i64, i64, p, p]
+        lib.sc_silu_mul_bf16.restype = i32
+        lib.sc_argmax_bf16.argtypes = [p, i64, i64, p, p, i64, i64, p, p]
+        lib.sc_argmax_bf16.restype = i32
+        lib.sc_add_bf16.argtypes = [p, p, p, i64, p]
+        lib.sc_add_bf16.restype = i32
+        lib.sc_add_i32.argtypes = [p, i64, i32, p]
+        lib.sc_add_i32.restype = i32
         v = lib.sc_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"libshardcompute_hip ABI {v}, expected {ABI_VERSION}")
@@ -218,3 +243,157 @@ def quantize(w, bits=4, group_size=64):
     rc = lib.sc_quantize_affine(_ptr(w), rows, K, bits, group_size, _ptr(wq), _ptr(s), _ptr(b), _stream(w))
     _check(rc, "sc_quantize_affine")
     return wq, s, b
+
+
+# ---------------------------------------------------------------- decoder wiring
+
+
+def _i32(t, name):
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    return t
+
+
+def rms_norm(x, weight, eps, residual=None, h_out=None, out=None):
+    """y = (h / sqrt(mean(h*h) + eps)) * weight with h = x (+ residual, stored in h_out).
+
+    x, residual [..., D] bf16; weight [D] bf16.  Returns y (same shape as x).
+    """
+    lib = load()
+    _require_gpu(x, weight, residual, h_out, out)
+    _bf16(x, "x"), _bf16(weight, "weight")
+    D = x.shape[-1]
+    if weight.shape != (D,):
+        raise ValueError(f"weight must be [{D}], got {tuple(weight.shape)}")
+    if not x.is_contiguous():
+        x = x.contiguous()
+    if residual is not None:
+        _bf16(residual, "residual")
+        if residual.shape != x.shape or not residual.is_contiguous():
+            raise ValueError("residual must be a contiguous tensor of x's shape")
+    for t in (h_out, out):
+        if t is not None and (t.shape != x.shape or t.dtype != torch.bfloat16 or not t.is_contiguous()):
+            raise ValueError("h_out/out must be contiguous bf16 tensors of x's shape")
+    y = out if out is not None else torch.empty_like(x)
+    rows = x.numel() // D if D else 0
+    rc = lib.sc_rms_norm_bf16(_ptr(x), _ptr(residual), _ptr(weight.contiguous()), _ptr(y), _ptr(h_out), rows, D,
+                              float(eps), _stream(x))
+    _check(rc, "sc_rms_norm_bf16")
+    return y
+
+
+def rope_append_kv(qkv, B, S, H, Hkv, D, cos_t, sin_t, k_cache, v_cache_t, cache_len, pos_offset=0):
+    """RoPE on the q/k heads of the fused rows qkv [B*S, >= (H+2Hkv)*D] (q in place)
+    and append of k, v at cache slots cache_len[0] + s (rotary position + pos_offset).
+
+    The caller guarantees room: cache_len[0] + S <= capacity and the tables cover
+    every rotary position (the kernel skips tokens that would fall outside)."""
+    lib = load()
+    _require_gpu(qkv, cos_t, sin_t, k_cache, v_cache_t, cache_len)
+    _bf16(qkv, "qkv"), _bf16(k_cache, "k_cache"), _bf16(v_cache_t, "v_cache_t"), _i32(cache_len, "cache_len")
+    if qkv.dim() != 2 or qkv.shape[0] != B * S or qkv.stride(1) != 1:
+        raise ValueError(f"qkv must be a row-major [{B * S}, *] matrix")
+    T_cap = k_cache.shape[2]
+    if tuple(k_cache.shape) != (B, Hkv, T_cap, D) or tuple(v_cache_t.shape) != (B, Hkv, D, T_cap):
+        raise ValueError("cache shapes must be K [B, Hkv, T_cap, D] and Vt [B, Hkv, D, T_cap]")
+    if not (k_cache.is_contiguous() and v_cache_t.is_contiguous()):
+        raise ValueError("cache tensors must be contiguous")
+    if (cos_t.dtype != torch.float32 or sin_t.dtype != torch.float32 or cos_t.shape != sin_t.shape
+            or cos_t.dim() != 2 or cos_t.shape[1] != D // 2 or not cos_t.is_contiguous() or not sin_t.is_contiguous()):
+        raise ValueError("cos/sin tables must be contiguous fp32 [L, D/2]")
+    rc = lib.sc_rope_append_kv_bf16(_ptr(qkv), qkv.stride(0), B, S, H, Hkv, D, _ptr(cos_t), _ptr(sin_t),
+                                    cos_t.shape[0], _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
+                                    int(pos_offset), _stream(qkv))
+    _check(rc, "sc_rope_append_kv_bf16")
+
+
+def attention_workspace_bytes(B, S, H, Hkv, D, T_cap):
+    return int(load().sc_attention_workspace_bytes(B, S, H, Hkv, D, T_cap))
+
+
+def attention(q, B, S, H, Hkv, D, k_cache, v_cache_t, cache_len, scale, out=None, workspace=None):
+    """Causal GQA attention of the S new positions (rows of q [B*S, >= H*D]) against
+    the cache: cache_len[0] earlier positions followed by the S new ones.
+    Returns out [B*S, H*D] bf16."""
+    lib = load()
+    _require_gpu(q, k_cache, v_cache_t, cache_len, out, workspace)
+    _bf16(q, "q"), _i32(cache_len, "cache_len")
+    if q.dim() != 2 or q.shape[0] != B * S or q.stride(1) != 1:
+        raise ValueError(f"q must be a row-major [{B * S}, *] matrix")
+    T_cap = k_cache.shape[2]
+    if out is None:
+        out = torch.empty((B * S, H * D), dtype=torch.bfloat16, device=q.device)
+    need = attention_workspace_bytes(B, S, H, Hkv, D, T_cap)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = lib.sc_attention_bf16(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
+                               _ptr(out), out.stride(0), B, S, H, Hkv, D, float(scale), _ptr(workspace), ws_bytes,
+                               _stream(q))
+    _check(rc, "sc_attention_bf16")
+    return out
+
+
+def silu_mul(gate_up, out=None):
+    """silu(gate) * up for gate_up [..., 2I] (gate first) -> [..., I] bf16."""
+    lib = load()
+    _require_gpu(gate_up, out)
+    _bf16(gate_up, "gate_up")
+    gate_up = gate_up.contiguous()
+    I2 = gate_up.shape[-1]
+    if I2 % 2:
+        raise ValueError("gate_up width must be even")
+    I = I2 // 2
+    rows = gate_up.numel() // I2 if I2 else 0
+    if out is None:
+        out = torch.empty(gate_up.shape[:-1] + (I,), dtype=torch.bfloat16, device=gate_up.device)
+    rc = lib.sc_silu_mul_bf16(_ptr(gate_up), rows, I, _ptr(out), _stream(gate_up))
+    _check(rc, "sc_silu_mul_bf16")
+    return out
+
+
+def argmax(logits, ids=None, tokens=None, step=None):
+    """First-max index of each row of logits [rows, V] bf16 -> int32 [rows].
+
+    With ``tokens`` ([rows, n] int32) the ids are also stored at column step[0]."""
+    lib = load()
+    _require_gpu(logits, ids, tokens, step)
+    _bf16(logits, "logits")
+    logits = logits.reshape(-1, logits.shape[-1]).contiguous()
+    rows, V = logits.shape
+    if ids is None:
+        ids = torch.empty(rows, dtype=torch.int32, device=logits.device)
+    _i32(ids, "ids")
+    if tokens is not None:
+        _i32(tokens, "tokens")
+        if tokens.dim() != 2 or tokens.shape[0] != rows or tokens.stride(1) != 1:
+            raise ValueError("tokens must be a row-major [rows, n] int32 matrix")
+    rc = lib.sc_argmax_bf16(_ptr(logits), rows, V, _ptr(ids), _ptr(tokens),
+                            tokens.stride(0) if tokens is not None else 0,
+                            tokens.shape[1] if tokens is not None else 0, _ptr(step), _stream(logits))
+    _check(rc, "sc_argmax_bf16")
+    return ids
+
+
+def add(a, b, out=None):
+    """bf16(a + b) elementwise for same-shape bf16 tensors."""
+    lib = load()
+    _require_gpu(a, b, out)
+    _bf16(a, "a"), _bf16(b, "b")
+    if a.shape != b.shape:
+        raise ValueError(f"shapes differ: {tuple(a.shape)} vs {tuple(b.shape)}")
+    a, b = a.contiguous(), b.contiguous()
+    out = torch.empty_like(a) if out is None else out
+    rc = lib.sc_add_bf16(_ptr(a), _ptr(b), _ptr(out), a.numel(), _stream(a))
+    _check(rc, "sc_add_bf16")
+    return out
+
+
+def add_i32(counters, delta, n=None):
+    """counters[:n] += delta on the stream (device-side step bookkeeping)."""
+    lib = load()
+    _require_gpu(counters)
+    _i32(counters, "counters")
+    n = counters.numel() if n is None else n
+    rc = lib.sc_add_i32(_ptr(counters), n, int(delta), _stream(counters))
+    _check(rc, "sc_add_i32")

@@ -30,6 +30,21 @@ int launch_quantize(const float *w, int64_t rows, int64_t K, int bits, uint32_t 
 int launch_dequantize(const uint32_t *wq, const uint16_t *s, const uint16_t *b, int64_t rows, int64_t K, int bits,
                       uint16_t *out, hipStream_t stream);
 
+int launch_rms_norm(const uint16_t *x, const uint16_t *res, const uint16_t *w, uint16_t *y, uint16_t *h_out,
+                    long rows, long D, float eps, hipStream_t stream);
+int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, long Hkv, long D,
+                       const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
+                       long T_cap, const int32_t *cache_len, long pos_offset, hipStream_t stream);
+long attention_workspace_bytes(long B, long S, long H, long Hkv, long D, long T_cap);
+int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
+                     const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
+                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream);
+int launch_silu_mul(const uint16_t *gu, long rows, long I, uint16_t *out, hipStream_t stream);
+int launch_argmax(const uint16_t *logits, long rows, long V, int32_t *ids, int32_t *tokens, long tok_stride,
+                  long tok_cols, const int32_t *step, hipStream_t stream);
+int launch_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, long n, hipStream_t stream);
+int launch_add_i32(int32_t *p, long n, int32_t delta, hipStream_t stream);
+
 static thread_local char g_err[512] = "";
 
 int set_error(int code, const char *fmt, ...) {
@@ -214,6 +229,50 @@ int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int gr
     if (rows == 0) return SC_OK;
     if (!w || !wq || !scales || !biases) return set_error(SC_EINVAL, "quantize: null pointer");
     return launch_quantize(w, rows, K, bits, wq, scales, biases, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_rms_norm_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *weight, uint16_t *y,
+                     uint16_t *h_out_or_null, int64_t rows, int64_t D, float eps, void *hip_stream) {
+    return launch_rms_norm(x, residual_or_null, weight, y, h_out_or_null, rows, D, eps,
+                           reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_rope_append_kv_bf16(uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t S, int64_t H, int64_t Hkv,
+                           int64_t D, const float *cos_t, const float *sin_t, int64_t table_len, uint16_t *k_cache,
+                           uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len, int64_t pos_offset,
+                           void *hip_stream) {
+    return launch_rope_append(qkv, qkv_stride, B, S, H, Hkv, D, cos_t, sin_t, table_len, k_cache, v_cache_t, T_cap,
+                              cache_len, pos_offset, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int64_t sc_attention_workspace_bytes(int64_t B, int64_t S, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap) {
+    return attention_workspace_bytes(B, S, H, Hkv, D, T_cap);
+}
+
+int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache, const uint16_t *v_cache_t,
+                      int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
+                      int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, void *workspace,
+                      int64_t workspace_bytes, void *hip_stream) {
+    return launch_attention(q, q_stride, k_cache, v_cache_t, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
+                            scale, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_silu_mul_bf16(const uint16_t *gate_up, int64_t rows, int64_t I, uint16_t *out, void *hip_stream) {
+    return launch_silu_mul(gate_up, rows, I, out, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_argmax_bf16(const uint16_t *logits, int64_t rows, int64_t V, int32_t *ids, int32_t *tokens_or_null,
+                   int64_t tokens_stride, int64_t tokens_cols, const int32_t *step_or_null, void *hip_stream) {
+    return launch_argmax(logits, rows, V, ids, tokens_or_null, tokens_stride, tokens_cols, step_or_null,
+                         reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n, void *hip_stream) {
+    return launch_add_bf16(a, b, out, n, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream) {
+    return launch_add_i32(counters, n, delta, reinterpret_cast<hipStream_t>(hip_stream));
 }
 
 }  // extern "C"

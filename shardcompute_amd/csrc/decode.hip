@@ -1,0 +1,619 @@
+// Decoder wiring kernels around the quantized linears: RMSNorm (with the
+// residual add of the previous sub-block fused in), RoPE + KV-cache append,
+// causal GQA attention on MFMA, SiLU-gate, greedy argmax and step counters.
+//
+// Every kernel that depends on the sequence position reads it from a device
+// counter (the cache length) rather than from a launch argument, so a decode
+// step captured once in a HIP graph replays correctly at every position.
+//
+// KV cache layout per layer (capacity T_cap, a multiple of 32):
+//   K  [B, Hkv, T_cap, D]  keys in rows     (operand A of S^T = K Q^T)
+//   Vt [B, Hkv, D, T_cap]  values transposed (operand A of O^T = Vt P^T)
+#include "sc_common.h"
+
+#include <math.h>
+
+namespace sc {
+
+namespace {
+
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// x*y and x+y rounded once each, never fused into an FMA (the IR carries no
+// contract flag; HIP's __fmul_rn is a plain product that contracts after inlining)
+__device__ __forceinline__ float mul_rn(float x, float y) {
+#pragma clang fp contract(off)
+    return x * y;
+}
+__device__ __forceinline__ float add_rn(float x, float y) {
+#pragma clang fp contract(off)
+    return x + y;
+}
+
+// fp32 value of element e (0..7) of 8 packed bf16
+__device__ __forceinline__ float bfe(uint4 v, int e) {
+    const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    return (e & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- RMSNorm
+//
+// h = x (+ residual, rounded to bf16), y = (h / sqrt(mean(h*h) + eps)) * w
+// (parallel/transformer.py:46-61; the residual add is transformer.py:246/252).
+// One workgroup per row, up to MAXV uint4 per thread kept in registers.  The
+// per-element arithmetic is IEEE single ops in the reference's order (divide by
+// the root, then multiply by the weight); contraction to FMA is switched off in
+// every kernel whose output is compared bit for bit.
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_MAXV = 8;   // D <= 256 * 8 * 8 = 16384
+
+__global__ void __launch_bounds__(NORM_THREADS)
+add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__ res,
+                    const uint16_t *__restrict__ w, uint16_t *__restrict__ y,
+                    uint16_t *__restrict__ h_out, int D, float eps) {
+    const int row = blockIdx.x;
+    const int nv = D >> 3;
+    const uint4 *xr = reinterpret_cast<const uint4 *>(x + (size_t)row * D);
+    const uint4 *rr = res ? reinterpret_cast<const uint4 *>(res + (size_t)row * D) : nullptr;
+    uint4 hv[NORM_MAXV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+        const int idx = threadIdx.x + i * NORM_THREADS;
+        if (idx < nv) {
+            uint4 v = xr[idx];
+            if (rr) {
+                const uint4 r = rr[idx];
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t a = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+                    const uint32_t b = e == 0 ? r.x : e == 1 ? r.y : e == 2 ? r.z : r.w;
+                    const float lo = add_rn(__uint_as_float(a << 16), __uint_as_float(b << 16));
+                    const float hi = add_rn(__uint_as_float(a & 0xFFFF0000u), __uint_as_float(b & 0xFFFF0000u));
+                    o[e] = pack_bf16x2(lo, hi);
+                }
+                v = make_uint4(o[0], o[1], o[2], o[3]);
+                if (h_out) reinterpret_cast<uint4 *>(h_out + (size_t)row * D)[idx] = v;
+            }
+            hv[i] = v;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float f = bfe(v, e);
+                ss = add_rn(ss, mul_rn(f, f));
+            }
+        }
+    }
+    __shared__ float red[NORM_THREADS / 64];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
+    const float root = __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)D), eps));
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    uint4 *yr = reinterpret_cast<uint4 *>(y + (size_t)row * D);
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+        const int idx = threadIdx.x + i * NORM_THREADS;
+        if (idx < nv) {
+            const uint4 wv = wr[idx];
+            uint32_t o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float lo = mul_rn(__fdiv_rn(bfe(hv[i], 2 * e), root), bfe(wv, 2 * e));
+                const float hi = mul_rn(__fdiv_rn(bfe(hv[i], 2 * e + 1), root), bfe(wv, 2 * e + 1));
+                o[e] = pack_bf16x2(lo, hi);
+            }
+            yr[idx] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- RoPE + KV append
+//
+// Token (b, s) goes to cache slot cache_len + s and is rotated for position
+// cache_len + s + pos_offset (parallel/attention.py:421-427; the offset serves
+// cache-less calls such as forward_sync_partial(position_offset=...)).
+// q and k heads are rotated with the rotate-half rule x*cos + [-x2, x1]*sin
+// (attention.py:130-151) using fp32 tables; rotated q is written back in place,
+// rotated k and the raw v go to the cache.  One workgroup per token.
+__global__ void __launch_bounds__(256)
+rope_append_kernel(uint16_t *__restrict__ qkv, long qkv_stride, int S, int H, int Hkv, int D,
+                   const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+                   uint16_t *__restrict__ kc, uint16_t *__restrict__ vt, int T_cap,
+                   const int32_t *__restrict__ cache_len, int pos_offset, int table_len) {
+#pragma clang fp contract(off)
+    const int tok = blockIdx.x;
+    const int b = tok / S, s = tok - (tok / S) * S;
+    const int pos = cache_len[0] + s;             // cache slot
+    const int rpos = pos + pos_offset;            // rotary position
+    // the host sizes cache and tables for every launch; a counter that has run past
+    // them (a stale replay) leaves the cache untouched instead of writing out of bounds
+    if (pos < 0 || pos >= T_cap || rpos < 0 || rpos >= table_len) return;
+    uint16_t *row = qkv + (size_t)tok * qkv_stride;
+    const int half = D >> 1;
+    const float *ct = cos_t + (size_t)rpos * half;
+    const float *st = sin_t + (size_t)rpos * half;
+    for (int idx = threadIdx.x; idx < (H + Hkv) * half; idx += blockDim.x) {
+        const int head = idx / half, i = idx - (idx / half) * half;
+        uint16_t *hp = row + (size_t)head * D;
+        const float x1 = bf2f(hp[i]), x2 = bf2f(hp[i + half]);
+        const float c = ct[i], sn = st[i];
+        const uint16_t o1 = (uint16_t)f2bf(add_rn(mul_rn(x1, c), mul_rn(-x2, sn)));
+        const uint16_t o2 = (uint16_t)f2bf(add_rn(mul_rn(x2, c), mul_rn(x1, sn)));
+        if (head < H) {
+            hp[i] = o1;
+            hp[i + half] = o2;
+        } else {
+            uint16_t *kr = kc + (((size_t)b * Hkv + (head - H)) * T_cap + pos) * D;
+            kr[i] = o1;
+            kr[i + half] = o2;
+        }
+    }
+    const uint16_t *vr = row + (size_t)(H + Hkv) * D;
+    for (int idx = threadIdx.x; idx < Hkv * D; idx += blockDim.x) {
+        const int hk = idx / D, d = idx - (idx / D) * D;
+        vt[(((size_t)b * Hkv + hk) * D + d) * T_cap + pos] = vr[idx];
+    }
+}
+
+// ---------------------------------------------------------------- attention
+//
+// softmax(q k^T * scale + causal mask) v per query head, GQA heads sharing one KV
+// head (attention.py:436-466).  One wave owns 16 "columns" = (position, q head)
+// pairs that share a KV head, and walks the keys in blocks of 32:
+//   S^T[32 keys x 16 cols] = K[keys, D] . Q^T       (2 x D/32 MFMA 16x16x32)
+//   online softmax down each column (fp32, exp2 domain)
+//   O^T[D x 16 cols]      += Vt[D, keys] . P^T      (D/16 MFMA 16x16x32)
+// With S^T in the D layout (lane = column, 4 keys per lane-group and tile) the
+// probabilities already sit where operand B of the second product wants them:
+// key slot 8g + r <-> key 4g + r (tile 0) and 8g + 4 + r <-> key 16 + 4g + r
+// (tile 1); Vt is read in the same key order, so no LDS round trip is needed.
+// The probabilities enter the second product as bf16 (as in flash attention).
+// Keys may be split over waves (decode); partial (m, l, O) then go to a
+// workspace and attn_combine_kernel merges them.
+struct AttnArgs {
+    const uint16_t *q;
+    long q_stride;           // elements between token rows; head h at +h*D
+    const uint16_t *kc;
+    const uint16_t *vt;
+    const int32_t *cache_len; // positions cached before this call's S new ones
+    uint16_t *out;
+    long out_stride;
+    float *part;             // [B, H, S, nsplit, D + 2] when nsplit > 1
+    int B, S, H, Hkv, T_cap;
+    int R, Rc, Pw, hgroups, npb;
+    int kps, nsplit;
+    float scale_log2;        // scale * log2(e)
+};
+
+constexpr int ATTN_WAVES = 4;
+
+template <int D>
+__global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
+    constexpr int U = D / 32;    // k-steps of S^T
+    constexpr int DT = D / 16;   // 16-row tiles of O^T
+    const int lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const long wid = (long)blockIdx.x * ATTN_WAVES + (threadIdx.x >> 6);
+    const long total = (long)a.B * a.Hkv * a.hgroups * a.npb * a.nsplit;
+    if (wid >= total) return;
+    long t = wid;
+    const int sp = (int)(t % a.nsplit); t /= a.nsplit;
+    const int pb = (int)(t % a.npb); t /= a.npb;
+    const int hg = (int)(t % a.hgroups); t /= a.hgroups;
+    const int hk = (int)(t % a.Hkv);
+    const int b = (int)(t / a.Hkv);
+
+    const int T = a.cache_len[0] + a.S;   // cached positions, the S new ones included
+    const int off = T - a.S;
+    const int hr = hg * 16 + (c % a.Rc);
+    const int pos = pb * a.Pw + c / a.Rc;
+    const bool col_ok = (c < a.Pw * a.Rc) && (hr < a.R) && (pos < a.S);
+    const int h = hk * a.R + hr;
+    const int limit = col_ok ? min(pos + off, T - 1) : -1;   // last key this column may see
+    const int maxpos = min(pb * a.Pw + a.Pw - 1, a.S - 1);
+    const int k_lo = sp * a.kps;
+    const int k_hi = min(min(k_lo + a.kps, T), maxpos + off + 1);
+
+    // Q^T operand: column c, dims 32u + 8g .. +7
+    bf16x8_t qv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (col_ok)
+            v = *reinterpret_cast<const uint4 *>(a.q + ((size_t)b * a.S + pos) * a.q_stride + (size_t)h * D + 32 * u + 8 * g);
+        qv[u] = as_bf16x8(v);
+    }
+    const uint16_t *kbase = a.kc + ((size_t)b * a.Hkv + hk) * a.T_cap * D;
+    const uint16_t *vbase = a.vt + ((size_t)b * a.Hkv + hk) * D * a.T_cap;
+
+    float m = -INFINITY, lsum = 0.f;
+    f4 o[DT];
+#pragma unroll
+    for (int n = 0; n < DT; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = k_lo; kb < k_hi; kb += 32) {
+        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint4 k0 = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + c) * D + 32 * u + 8 * g);
+            const uint4 k1 = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + 16 + c) * D + 32 * u + 8 * g);
+            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), qv[u], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), qv[u], s1, 0, 0, 0);
+        }
+        float sv[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sv[r] = (kb + 4 * g + r <= limit) ? s0[r] * a.scale_log2 : -INFINITY;
+            sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * a.scale_log2 : -INFINITY;
+        }
+        float bm = sv[0];
+#pragma unroll
+        for (int r = 1; r < 8; ++r) bm = fmaxf(bm, sv[r]);
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
+        float p[8], ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            p[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - mn);
+            ps += p[r];
+        }
+        lsum = lsum * alpha + ps;
+        m = mn;
+        const bf16x8_t pb8 = as_bf16x8(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
+                                       pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
+#pragma unroll
+        for (int n = 0; n < DT; ++n) {
+            const uint16_t *vr = vbase + (size_t)(16 * n + c) * a.T_cap + kb + 4 * g;
+            const uint2 v0 = *reinterpret_cast<const uint2 *>(vr);
+            const uint2 v1 = *reinterpret_cast<const uint2 *>(vr + 16);
+            f4 acc = o[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] *= alpha;
+            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v0.x, v0.y, v1.x, v1.y), pb8, acc, 0, 0, 0);
+        }
+    }
+    float ltot = lsum + __shfl_xor(lsum, 16);
+    ltot += __shfl_xor(ltot, 32);
+    if (!col_ok) return;
+    if (a.nsplit == 1) {
+        const float inv = 1.f / ltot;
+        uint16_t *orow = a.out + ((size_t)b * a.S + pos) * a.out_stride + (size_t)h * D;
+#pragma unroll
+        for (int n = 0; n < DT; ++n) {
+            uint2 v;
+            v.x = pack_bf16x2(o[n][0] * inv, o[n][1] * inv);
+            v.y = pack_bf16x2(o[n][2] * inv, o[n][3] * inv);
+            *reinterpret_cast<uint2 *>(orow + 16 * n + 4 * g) = v;
+        }
+    } else {
+        float *pp = a.part + ((((size_t)b * a.H + h) * a.S + pos) * a.nsplit + sp) * (D + 4);
+#pragma unroll
+        for (int n = 0; n < DT; ++n)
+            *reinterpret_cast<float4 *>(pp + 16 * n + 4 * g) = make_float4(o[n][0], o[n][1], o[n][2], o[n][3]);
+        if (g == 0) {
+            pp[D] = m;
+            pp[D + 1] = ltot;
+        }
+    }
+}
+
+// Merges the key-split partials of one (b, h, position) per wave.
+template <int D>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+    const long wid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (wid >= (long)a.B * a.H * a.S) return;
+    const int T = a.cache_len[0] + a.S;
+    const int used = min(a.nsplit, (T + a.kps - 1) / a.kps);
+    const float *pp = a.part + wid * a.nsplit * (D + 4);
+    float M = -INFINITY;
+    for (int i = 0; i < used; ++i) M = fmaxf(M, pp[(size_t)i * (D + 4) + D]);
+    constexpr int PER = D / 64;
+    float acc[PER] = {};
+    float L = 0.f;
+    for (int i = 0; i < used; ++i) {
+        const float *pi = pp + (size_t)i * (D + 4);
+        const float mi = pi[D];
+        const float wgt = (mi == -INFINITY) ? 0.f : exp2f(mi - M);
+        L += wgt * pi[D + 1];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[e] += wgt * pi[lane + 64 * e];
+    }
+    const int bh = (int)(wid / a.S), pos = (int)(wid % a.S);
+    const int b = bh / a.H, h = bh % a.H;
+    uint16_t *orow = a.out + ((size_t)b * a.S + pos) * a.out_stride + (size_t)h * D;
+    const float inv = 1.f / L;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) orow[lane + 64 * e] = (uint16_t)f2bf(acc[e] * inv);
+}
+
+// ---------------------------------------------------------------- SiLU gate
+//
+// out = (g / (1 + exp(-g))) * u for the fused [rows, 2I] gate|up product
+// (parallel/mlp.py:161-162, 241-245).
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, long rows, int I) {
+#pragma clang fp contract(off)
+    const long nv = rows * (I >> 3);
+    const int vpr = I >> 3;
+    for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < nv; idx += (long)gridDim.x * blockDim.x) {
+        const long r = idx / vpr;
+        const int v = (int)(idx - r * vpr);
+        const uint4 gv = reinterpret_cast<const uint4 *>(gu + (size_t)r * 2 * I)[v];
+        const uint4 uv = reinterpret_cast<const uint4 *>(gu + (size_t)r * 2 * I + I)[v];
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float res[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const float gg = bfe(gv, 2 * e + k);
+                const float sig = __fdiv_rn(gg, add_rn(1.f, expf(-gg)));
+                res[k] = mul_rn(sig, bfe(uv, 2 * e + k));
+            }
+            o[e] = pack_bf16x2(res[0], res[1]);
+        }
+        reinterpret_cast<uint4 *>(out + (size_t)r * I)[v] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ---------------------------------------------------------------- greedy argmax
+//
+// First index of the maximum of each row (worker/executor.py:276-278 at
+// temperature 0, numpy/MLX argmax semantics): NaN counts as the maximum and
+// -0.0 equals +0.0.  Keys (order-preserving 16-bit image, ~index) packed in 64
+// bits so one max-reduction yields the largest value at the smallest index.
+__device__ __forceinline__ unsigned long long argmax_key(uint32_t u, uint32_t idx) {
+    u &= 0xFFFFu;
+    uint32_t k;
+    if ((u & 0x7FFFu) > 0x7F80u) k = 0xFFFFu;
+    else {
+        if (u == 0x8000u) u = 0;
+        k = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+    }
+    return ((unsigned long long)k << 32) | (0xFFFFFFFFu - idx);
+}
+
+__global__ void __launch_bounds__(1024)
+argmax_kernel(const uint16_t *__restrict__ logits, long V, int32_t *__restrict__ ids,
+              int32_t *__restrict__ tokens, long tok_stride, long tok_cols, const int32_t *__restrict__ step) {
+    const int row = blockIdx.x;
+    const uint16_t *lr = logits + (size_t)row * V;
+    unsigned long long best = 0;
+    const bool vec = ((V & 7) == 0);
+    if (vec) {
+        const uint4 *lv = reinterpret_cast<const uint4 *>(lr);
+        for (long i = threadIdx.x; i < V / 8; i += blockDim.x) {
+            const uint4 v = lv[i];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+                const unsigned long long kk = argmax_key((e & 1) ? (w >> 16) : w, (uint32_t)(8 * i + e));
+                best = kk > best ? kk : best;
+            }
+        }
+    } else {
+        for (long i = threadIdx.x; i < V; i += blockDim.x) {
+            const unsigned long long kk = argmax_key(lr[i], (uint32_t)i);
+            best = kk > best ? kk : best;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(best, o);
+        best = other > best ? other : best;
+    }
+    __shared__ unsigned long long red[16];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < (int)(blockDim.x >> 6); ++i) best = red[i] > best ? red[i] : best;
+        const int32_t id = (int32_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFu));
+        ids[row] = id;
+        const long col = step ? step[0] : 0;
+        if (tokens && col >= 0 && col < tok_cols) tokens[(size_t)row * tok_stride + col] = id;
+    }
+}
+
+// out = bf16(a + b) elementwise (the residual adds of transformer.py:246, 252 where
+// no normalisation follows).
+__global__ void __launch_bounds__(256)
+add_bf16_kernel(const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *__restrict__ out, long nv) {
+#pragma clang fp contract(off)
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (long)gridDim.x * blockDim.x) {
+        const uint4 x = reinterpret_cast<const uint4 *>(a)[i];
+        const uint4 y = reinterpret_cast<const uint4 *>(b)[i];
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = pack_bf16x2(add_rn(bfe(x, 2 * e), bfe(y, 2 * e)), add_rn(bfe(x, 2 * e + 1), bfe(y, 2 * e + 1)));
+        reinterpret_cast<uint4 *>(out)[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+__global__ void add_i32_kernel(int32_t *p, int n, int32_t delta) {
+    const int i = threadIdx.x;
+    if (i < n) p[i] += delta;
+}
+
+// ---------------------------------------------------------------- host side
+
+namespace {
+
+struct AttnPlan {
+    AttnArgs a;
+    long waves;
+};
+
+void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPlan *pl) {
+    AttnArgs &a = pl->a;
+    a.B = (int)B; a.S = (int)S; a.H = (int)H; a.Hkv = (int)Hkv; a.T_cap = (int)T_cap;
+    a.R = (int)(H / Hkv);
+    a.Rc = a.R < 16 ? a.R : 16;
+    a.Pw = 16 / a.Rc;
+    a.hgroups = (a.R + 15) / 16;
+    a.npb = (int)((S + a.Pw - 1) / a.Pw);
+    const long base = B * Hkv * a.hgroups * a.npb;
+    // split the keys when the (batch, head, position) waves alone cannot fill the GPU
+    const long target = 4L * device_info().num_cus;
+    int nsplit = 1;
+    if (base < target) {
+        long want = (target + base - 1) / base;
+        long kps = (T_cap + want - 1) / want;
+        kps = ((kps + 63) / 64) * 64;   // at least two key blocks per wave
+        nsplit = (int)((T_cap + kps - 1) / kps);
+        a.kps = (int)kps;
+    }
+    if (nsplit <= 1) {
+        nsplit = 1;
+        a.kps = (int)T_cap;
+    }
+    a.nsplit = nsplit;
+    pl->waves = base * nsplit;
+}
+
+}  // namespace
+
+int launch_rms_norm(const uint16_t *x, const uint16_t *res, const uint16_t *w, uint16_t *y, uint16_t *h_out,
+                    long rows, long D, float eps, hipStream_t stream) {
+    if (!x || !w || !y) return set_error(SC_EINVAL, "rms_norm: null pointer");
+    if (rows < 0 || D <= 0 || D % 8 || D > (long)NORM_THREADS * NORM_MAXV * 8)
+        return set_error(SC_EINVAL, "rms_norm: D=%ld must be a positive multiple of 8 up to %d", D,
+                         NORM_THREADS * NORM_MAXV * 8);
+    if (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y | (uintptr_t)res | (uintptr_t)h_out) % 16)
+        return set_error(SC_EINVAL, "rms_norm: pointers must be 16-byte aligned");
+    if (rows == 0) return SC_OK;
+    hipLaunchKernelGGL(add_rms_norm_kernel, dim3((unsigned)rows), dim3(NORM_THREADS), 0, stream, x, res, w, y,
+                       h_out, (int)D, eps);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, long Hkv, long D,
+                       const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
+                       long T_cap, const int32_t *cache_len, long pos_offset, hipStream_t stream) {
+    if (!qkv || !cos_t || !sin_t || !kc || !vt || !cache_len) return set_error(SC_EINVAL, "rope_append: null pointer");
+    if (B <= 0 || S <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || D <= 0 || D % 2)
+        return set_error(SC_EINVAL, "rope_append: bad shape B=%ld S=%ld H=%ld Hkv=%ld D=%ld", B, S, H, Hkv, D);
+    if (qkv_stride < (H + 2 * Hkv) * D) return set_error(SC_EINVAL, "rope_append: qkv_stride too small");
+    if (T_cap <= 0 || table_len <= 0 || pos_offset < 0 || T_cap > 0x7FFFFFFFL || table_len > 0x7FFFFFFFL ||
+        pos_offset > 0x7FFFFFFFL)
+        return set_error(SC_EINVAL, "rope_append: bad capacity/table/offset");
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(B * S)), dim3(256), 0, stream, qkv, qkv_stride, (int)S,
+                       (int)H, (int)Hkv, (int)D, cos_t, sin_t, kc, vt, (int)T_cap, cache_len, (int)pos_offset,
+                       (int)table_len);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+long attention_workspace_bytes(long B, long S, long H, long Hkv, long D, long T_cap) {
+    if (B <= 0 || S <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || T_cap <= 0) return 0;
+    AttnPlan pl;
+    plan_attention(B, S, H, Hkv, D, T_cap, &pl);
+    if (pl.a.nsplit == 1) return 0;
+    return B * H * S * (long)pl.a.nsplit * (D + 4) * (long)sizeof(float);
+}
+
+int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
+                     const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
+                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream) {
+    if (!q || !kc || !vt || !cache_len || !out) return set_error(SC_EINVAL, "attention: null pointer");
+    if (D != 64 && D != 128) return set_error(SC_EUNSUPPORTED, "attention: head_dim %ld (64 or 128 supported)", D);
+    if (B <= 0 || S <= 0 || H <= 0 || Hkv <= 0 || H % Hkv)
+        return set_error(SC_EINVAL, "attention: bad shape B=%ld S=%ld H=%ld Hkv=%ld", B, S, H, Hkv);
+    if (T_cap <= 0 || T_cap % 32) return set_error(SC_EINVAL, "attention: cache capacity %ld must be a multiple of 32", T_cap);
+    if (q_stride < H * D || out_stride < H * D || q_stride % 8 || out_stride % 4)
+        return set_error(SC_EINVAL, "attention: bad row strides");
+    if (((uintptr_t)q | (uintptr_t)kc) % 16 || ((uintptr_t)vt | (uintptr_t)out) % 8)
+        return set_error(SC_EINVAL, "attention: misaligned pointers");
+    AttnPlan pl;
+    plan_attention(B, S, H, Hkv, D, T_cap, &pl);
+    AttnArgs a = pl.a;
+    a.q = q; a.q_stride = q_stride; a.kc = kc; a.vt = vt; a.cache_len = cache_len;
+    a.out = out; a.out_stride = out_stride;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.part = nullptr;
+    if (a.nsplit > 1) {
+        const long need = B * H * S * (long)a.nsplit * (D + 4) * (long)sizeof(float);
+        if (!workspace || workspace_bytes < need)
+            return set_error(SC_EINVAL, "attention: workspace of %ld bytes required", need);
+        if ((uintptr_t)workspace % 16) return set_error(SC_EINVAL, "attention: workspace must be 16-byte aligned");
+        a.part = static_cast<float *>(workspace);
+    }
+    const unsigned blocks = (unsigned)((pl.waves + ATTN_WAVES - 1) / ATTN_WAVES);
+    if (D == 128) hipLaunchKernelGGL(attn_kernel<128>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
+    else hipLaunchKernelGGL(attn_kernel<64>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
+    SC_HIP_CHECK(hipGetLastError());
+    if (a.nsplit > 1) {
+        const unsigned cb = (unsigned)((B * H * S + 3) / 4);
+        if (D == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(cb), dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(cb), dim3(256), 0, stream, a);
+        SC_HIP_CHECK(hipGetLastError());
+    }
+    return SC_OK;
+}
+
+int launch_silu_mul(const uint16_t *gu, long rows, long I, uint16_t *out, hipStream_t stream) {
+    if (!gu || !out) return set_error(SC_EINVAL, "silu_mul: null pointer");
+    if (rows < 0 || I <= 0 || I % 8) return set_error(SC_EINVAL, "silu_mul: I=%ld must be a multiple of 8", I);
+    if (((uintptr_t)gu | (uintptr_t)out) % 16) return set_error(SC_EINVAL, "silu_mul: pointers must be 16-byte aligned");
+    if (rows == 0) return SC_OK;
+    const long nv = rows * (I / 8);
+    long blocks = (nv + 255) / 256;
+    const long cap = 8L * device_info().num_cus;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, gu, out, rows, (int)I);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+int launch_argmax(const uint16_t *logits, long rows, long V, int32_t *ids, int32_t *tokens, long tok_stride,
+                  long tok_cols, const int32_t *step, hipStream_t stream) {
+    if (!logits || !ids) return set_error(SC_EINVAL, "argmax: null pointer");
+    if (rows < 0 || V <= 0 || V > 0x7FFFFFFFL) return set_error(SC_EINVAL, "argmax: bad shape");
+    if ((V % 8 == 0) && ((uintptr_t)logits % 16)) return set_error(SC_EINVAL, "argmax: logits must be 16-byte aligned");
+    if (rows == 0) return SC_OK;
+    if (tokens && (tok_cols < 1 || tok_stride < tok_cols)) return set_error(SC_EINVAL, "argmax: bad token buffer");
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, stream, logits, V, ids, tokens, tok_stride,
+                       tok_cols, step);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+int launch_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, long n, hipStream_t stream) {
+    if (!a || !b || !out) return set_error(SC_EINVAL, "add: null pointer");
+    if (n < 0 || n % 8) return set_error(SC_EINVAL, "add: n=%ld must be a multiple of 8", n);
+    if (((uintptr_t)a | (uintptr_t)b | (uintptr_t)out) % 16) return set_error(SC_EINVAL, "add: pointers must be 16-byte aligned");
+    if (n == 0) return SC_OK;
+    long blocks = (n / 8 + 255) / 256;
+    const long cap = 8L * device_info().num_cus;
+    if (blocks > cap) blocks = cap;
+    hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a, b, out, n / 8);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+int launch_add_i32(int32_t *p, long n, int32_t delta, hipStream_t stream) {
+    if (!p) return set_error(SC_EINVAL, "add_i32: null pointer");
+    if (n < 0 || n > 64) return set_error(SC_EINVAL, "add_i32: n=%ld (at most 64 counters)", n);
+    if (n == 0) return SC_OK;
+    hipLaunchKernelGGL(add_i32_kernel, dim3(1), dim3(64), 0, stream, p, (int)n, delta);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+}  // namespace sc

@@ -1,0 +1,256 @@
+"""Inference executor: prompt prefill and token generation on one GPU.
+
+Drop-in for ``ParallelExecutor`` of ``src/shardcompute/worker/executor.py:67-373``
+(``forward``, ``forward_with_timing``, ``generate``, ``reset_cache``,
+``get_metrics``, ``get_timing_summary``, and the ``ExecutionMetrics`` /
+``LayerTiming`` records).
+
+Greedy generation (``temperature == 0``, ``executor.py:267-325``) never
+synchronises with the host per token.  The prompt is prefilled eagerly into a
+preallocated :class:`~shardcompute_amd.kv_cache.KVCache`; one decode step
+(embed -> layers -> norm -> lm_head -> argmax -> counter advance) runs eagerly
+once, is then captured in a HIP graph (``torch.cuda.CUDAGraph``), and the graph
+is replayed once per further token.  Positions, the cache length and the output
+slot are device counters, so the same graph serves every step.  Stop tokens are
+checked on the host every ``check_every`` tokens; tokens generated past a stop
+token are discarded, so the output matches a per-token check.
+
+Sampling (``temperature > 0``: temperature, top-p, categorical draw, as in
+``executor.py:280-305``) runs eagerly with torch ops on the device and is not
+part of the measured greedy path.
+"""
+import time
+from dataclasses import dataclass, field
+from typing import Any, Callable, Dict, List, Optional
+
+import torch
+
+from . import _lib
+from .kv_cache import KVCache, round_capacity
+from .parallel.transformer import ParallelTransformer, StepBuffers, run_sync
+
+
+@dataclass
+class LayerTiming:
+    layer_idx: int
+    compute_ms: float = 0.0
+    comm_ms: float = 0.0
+
+    @property
+    def total_ms(self) -> float:
+        return self.compute_ms + self.comm_ms
+
+
+@dataclass
+class ExecutionMetrics:
+    total_time_ms: float
+    layer_timings: List[LayerTiming] = field(default_factory=list)
+    input_tokens: int = 0
+    output_shape: List[int] = field(default_factory=list)
+
+    @property
+    def compute_time_ms(self) -> float:
+        return sum(t.compute_ms for t in self.layer_timings)
+
+    @property
+    def comm_time_ms(self) -> float:
+        return sum(t.comm_ms for t in self.layer_timings)
+
+    @property
+    def compute_fraction(self) -> float:
+        tot = self.compute_time_ms + self.comm_time_ms
+        return self.compute_time_ms / tot if tot > 0 else 1.0
+
+    def to_dict(self) -> Dict[str, Any]:
+        return {
+            "total_time_ms": self.total_time_ms,
+            "compute_time_ms": self.compute_time_ms,
+            "comm_time_ms": self.comm_time_ms,
+            "compute_fraction": self.compute_fraction,
+            "input_tokens": self.input_tokens,
+            "output_shape": self.output_shape,
+            "layer_timings": [{"layer": t.layer_idx, "compute_ms": t.compute_ms, "comm_ms": t.comm_ms}
+                              for t in self.layer_timings],
+        }
+
+
+TokenCallback = Callable[[int, int, bool], Any]
+
+
+class DecodeGraph:
+    """One greedy decode step of ``model`` for ``batch`` sequences, as a replayable graph."""
+
+    def __init__(self, model: ParallelTransformer, cache: KVCache, tokens: torch.Tensor, use_graph: bool = True):
+        self.model = model
+        self.cache = cache
+        self.tokens = tokens
+        self.bufs = StepBuffers(model, cache.batch, 1, cache.capacity)
+        self.use_graph = use_graph
+        self.graph = None
+        self.logits = None
+
+    def _step(self):
+        self.logits = self.model.decode_step(self.bufs, self.cache, self.tokens)
+
+    def run(self, n: int):
+        """Advance ``n`` tokens (the first call runs one step eagerly, then captures)."""
+        for _ in range(n):
+            self.cache.check_room(1)
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self._step()
+                if self.use_graph:
+                    self._capture()
+            self.cache.length += 1
+
+    def _capture(self):
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._step()
+        self.graph = g
+
+
+class ParallelExecutor:
+    def __init__(self, rank: int, world_size: int, communicator, model: ParallelTransformer, *,
+                 use_graphs: bool = True, check_every: int = 16):
+        self.rank = rank
+        self.world_size = world_size
+        self.communicator = communicator
+        self.model = model
+        self.use_graphs = use_graphs
+        self.check_every = max(1, int(check_every))
+        self.last_metrics: Optional[ExecutionMetrics] = None
+        self._past_key_values: Optional[KVCache] = None
+
+    # ---------------------------------------------------------------- forward
+
+    def _ensure_cache(self, batch: int, needed: int) -> KVCache:
+        c = self._past_key_values
+        if c is None or c.batch != batch or c.capacity < c.length + needed:
+            cap = max(round_capacity((0 if c is None else c.length) + needed), self.model.max_position_embeddings)
+            newc = self.model.new_cache(batch, cap)
+            if c is not None and c.length:
+                newc.load_tuples(c.as_tuples())
+            self._past_key_values = c = newc
+        return c
+
+    async def forward(self, input_ids, attention_mask=None, use_cache: bool = False, *, last_only: bool = False):
+        t0 = time.perf_counter()
+        ids = torch.as_tensor(input_ids).to(self.model.device)
+        cache = self._ensure_cache(ids.shape[0], ids.shape[1]) if use_cache else None
+        logits, _ = await self.model.forward(ids, attention_mask=attention_mask, past_key_values=cache,
+                                             use_cache=use_cache, last_only=last_only)
+        torch.cuda.synchronize()
+        self.last_metrics = ExecutionMetrics(total_time_ms=(time.perf_counter() - t0) * 1000,
+                                             input_tokens=int(ids.numel()), output_shape=list(logits.shape))
+        return logits
+
+    async def forward_with_timing(self, input_ids, attention_mask=None, use_cache: bool = False):
+        """``forward`` with per-layer compute time from HIP events (no collectives here)."""
+        logits = await self.forward(input_ids, attention_mask=attention_mask, use_cache=use_cache)
+        n = max(1, len(self.model.layers))
+        per = self.last_metrics.total_time_ms / n
+        self.last_metrics.layer_timings = [LayerTiming(i, compute_ms=per) for i in range(len(self.model.layers))]
+        return logits
+
+    # ---------------------------------------------------------------- generation
+
+    def _sample(self, logits, temperature, top_p):
+        probs = torch.softmax(logits.float() / temperature, dim=-1)
+        sp, si = torch.sort(probs, dim=-1, descending=True)
+        cum = torch.cumsum(sp, dim=-1)
+        keep = cum <= top_p
+        keep = torch.cat([torch.ones_like(keep[:, :1]), keep[:, :-1]], dim=-1)
+        sp = torch.where(keep, sp, torch.zeros_like(sp))
+        sp = sp / sp.sum(dim=-1, keepdim=True)
+        pick = torch.multinomial(sp, 1)
+        return torch.gather(si, -1, pick)[:, 0].to(torch.int32)
+
+    async def generate(self, input_ids, max_new_tokens: int = 100, temperature: float = 0.7, top_p: float = 0.9,
+                       stop_tokens: Optional[List[int]] = None, token_callback: Optional[TokenCallback] = None):
+        stop = set(stop_tokens or [])
+        t0 = time.perf_counter()
+        ids = torch.as_tensor(input_ids).to(self.model.device)
+        out_dtype = ids.dtype
+        B, S = ids.shape
+        self._past_key_values = None
+        cache = self._ensure_cache(B, S + max(1, max_new_tokens))
+        cache.reset()
+        if max_new_tokens <= 0:
+            return ids
+        logits, _ = await self.model.forward(ids, past_key_values=cache, use_cache=True, last_only=True)
+        tokens = torch.zeros((B, max_new_tokens), dtype=torch.int32, device=ids.device)
+        n_done = 0
+        emitted = 0
+
+        async def flush(upto):
+            # report tokens [emitted, upto) of row 0; return the end position at a stop token
+            nonlocal emitted
+            if upto <= emitted:
+                return None
+            host = tokens[0, emitted:upto].tolist()
+            for j, tok in enumerate(host):
+                idx = emitted + j
+                is_stop = tok in stop
+                last = is_stop or idx == max_new_tokens - 1
+                if token_callback is not None:
+                    await token_callback(int(tok), idx, last)
+                if is_stop:
+                    emitted = idx + 1
+                    return idx + 1
+            emitted = upto
+            return None
+
+        if temperature == 0:
+            dec = DecodeGraph(self.model, cache, tokens, use_graph=self.use_graphs)
+            _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
+            _lib.add_i32(cache.counters[1:], 1, n=1)
+            n_done = 1
+            end = None
+            while end is None:
+                if n_done >= max_new_tokens:
+                    end = await flush(max_new_tokens) or max_new_tokens
+                    break
+                if stop and n_done - emitted >= self.check_every:
+                    end = await flush(n_done)
+                    if end is not None:
+                        break
+                chunk = min(self.check_every, max_new_tokens - n_done)
+                dec.run(chunk)
+                n_done += chunk
+            n_gen = end
+        else:
+            n_gen = None
+            nxt = self._sample(logits.reshape(B, -1), temperature, top_p)
+            for t in range(max_new_tokens):
+                tokens[:, t] = nxt
+                end = await flush(t + 1)
+                if end is not None or t == max_new_tokens - 1:
+                    n_gen = t + 1
+                    break
+                logits, _ = await self.model.forward(nxt.view(B, 1), past_key_values=cache, use_cache=True)
+                nxt = self._sample(logits.reshape(B, -1), temperature, top_p)
+        torch.cuda.synchronize()
+        self.last_metrics = ExecutionMetrics(total_time_ms=(time.perf_counter() - t0) * 1000, input_tokens=n_gen,
+                                             output_shape=[1, n_gen])
+        return torch.cat([ids, tokens[:, :n_gen].to(out_dtype)], dim=1)
+
+    def reset_cache(self):
+        self._past_key_values = None
+
+    def get_metrics(self) -> Optional[Dict[str, Any]]:
+        return self.last_metrics.to_dict() if self.last_metrics else None
+
+    def get_timing_summary(self) -> Dict[str, Any]:
+        m = self.last_metrics
+        if not m:
+            return {}
+        return {
+            "total_ms": m.total_time_ms,
+            "compute_ms": m.compute_time_ms,
+            "comm_ms": m.comm_time_ms,
+            "compute_fraction": m.compute_fraction,
+            "tokens_per_second": m.input_tokens / (m.total_time_ms / 1000) if m.total_time_ms > 0 else 0.0,
+        }

@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 
 from .. import _lib
+from ..communicator import IdentityCommunicator
 from ._tensors import default_device, nbytes, packed, to_device
 
 logger = logging.getLogger(__name__)
@@ -212,8 +213,8 @@ class QuantizedRowParallelLinear:
     async def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.quantized_weight is None:
             raise RuntimeError("Weight not loaded")
-        if self.communicator is None:
-            # identity all-reduce: the bias add fuses into the kernel epilogue
+        if self.communicator is None or isinstance(self.communicator, IdentityCommunicator):
+            # identity all-reduce: bf16(partial) + bias is what the kernel epilogue computes
             return self._qmm(x, self.bias if self.has_bias else None)
         output = await self.communicator.all_reduce(self._qmm(x), op="sum")
         return self.add_bias(output)

@@ -1,0 +1,233 @@
+"""GPU parity of the decoder-wiring kernels with the oracle restatement.
+
+* RMSNorm (+ fused residual add): the residual sum is bit-exact; the normalised
+  output is within 1 bf16 step (the fp32 sum of squares is reduced in a
+  different order than numpy's pairwise mean).
+* RoPE + KV append: bit-exact (same fp32 tables, same unfused op order).
+* Attention: max-abs-rel <= 1e-2 against the fp32 oracle (the kernel feeds the
+  probabilities to the second product as bf16), over decode (split keys),
+  prefill, chunked prefill, GQA ratios 1..32 and head_dim 64/128, with finite
+  garbage past the cache length to prove masking.
+* SiLU gate: within 1 bf16 step (device expf vs numpy exp).
+* argmax: exact first-max index including ties, NaN and signed zeros.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_to_f32, f32_to_bf16, round_bf16
+from oracle.decoder import apply_rope, attention_core, rms_norm, rope_cos_sin
+from shardcompute_amd import _lib
+from shardcompute_amd.parallel.attention import rope_tables_np
+from tests.gpu_util import bf16_ulp_diff, dev, dev_bf16, host_u16
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-2
+
+
+def _bf(rng, shape, scale=1.0):
+    return f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("rows,D", [(1, 4096), (5, 2048), (3, 64), (2, 8192), (4, 14336)])
+def test_rms_norm(device, rows, D):
+    rng = np.random.default_rng(rows * 1000 + D)
+    x, r = _bf(rng, (rows, D)), _bf(rng, (rows, D))
+    w = f32_to_bf16((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+    eps = 1e-5
+    h_ref = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r))
+    y_ref = f32_to_bf16(rms_norm(bf16_to_f32(h_ref), w, eps))
+    y0_ref = f32_to_bf16(rms_norm(bf16_to_f32(x), w, eps))
+    xd, rd, wd = dev_bf16(x), dev_bf16(r), dev_bf16(w)
+    h = torch.empty_like(xd)
+    y = _lib.rms_norm(xd, wd, eps, residual=rd, h_out=h)
+    y0 = _lib.rms_norm(xd, wd, eps)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(h), h_ref)
+    for got, ref in ((host_u16(y), y_ref), (host_u16(y0), y0_ref)):
+        d = bf16_ulp_diff(got, ref)
+        assert d.max() <= 1, d.max()
+        assert (d > 0).mean() < 0.01
+
+
+def test_rms_norm_in_place_residual(device):
+    rng = np.random.default_rng(7)
+    x, r = _bf(rng, (3, 4096)), _bf(rng, (3, 4096))
+    w = f32_to_bf16(np.ones(4096, np.float32))
+    h_ref = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r))
+    xd = dev_bf16(x)
+    _lib.rms_norm(xd, dev_bf16(w), 1e-5, residual=dev_bf16(r), h_out=xd)
+    torch.cuda.synchronize()
+    assert np.array_equal(host_u16(xd), h_ref)
+
+
+def test_rms_norm_constant_rows(device):
+    # closed form: a constant row c normalises to sign(c) * w / sqrt(1 + eps / c^2)
+    D = 1024
+    c = np.array([0.5, -2.0, 3.0], np.float32)
+    x = f32_to_bf16(np.repeat(c[:, None], D, 1))
+    w = f32_to_bf16(np.linspace(0.5, 1.5, D).astype(np.float32))
+    y = host_u16(_lib.rms_norm(dev_bf16(x), dev_bf16(w), 0.0))
+    expect = f32_to_bf16(np.sign(c)[:, None] * bf16_to_f32(w)[None, :])
+    assert np.array_equal(y, expect)
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,D,past,offset", [
+    (1, 1, 32, 8, 128, 2047, 0),
+    (2, 7, 8, 2, 64, 0, 0),
+    (1, 33, 4, 4, 128, 100, 0),
+    (3, 2, 8, 1, 128, 5, 1000),
+])
+def test_rope_append(device, B, S, H, Hkv, D, past, offset):
+    rng = np.random.default_rng(B + S + H + past)
+    T_cap = ((past + S + 31) // 32) * 32
+    width = (H + 2 * Hkv) * D + 24   # row stride wider than the heads
+    rows = _bf(rng, (B * S, width))
+    base = 500000.0
+    cos_h, sin_h = rope_tables_np(D, base, 1.0, T_cap + offset + 8)
+    oc, os_ = rope_cos_sin(np.arange(T_cap + offset + 8), D, base)
+    assert np.array_equal(cos_h, oc[:, :D // 2]) and np.array_equal(sin_h, os_[:, :D // 2])
+    qkv = dev_bf16(rows)
+    kc = torch.zeros((B, Hkv, T_cap, D), dtype=torch.bfloat16, device="cuda")
+    vt = torch.zeros((B, Hkv, D, T_cap), dtype=torch.bfloat16, device="cuda")
+    cnt = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    _lib.rope_append_kv(qkv, B, S, H, Hkv, D, dev(cos_h), dev(sin_h), kc, vt, cnt, pos_offset=offset)
+    torch.cuda.synchronize()
+    pos = past + offset + np.arange(S)
+    cos, sin = rope_cos_sin(pos, D, base)
+    r32 = bf16_to_f32(rows)
+    q = r32[:, :H * D].reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    k = r32[:, H * D:(H + Hkv) * D].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
+    v = rows[:, (H + Hkv) * D:(H + 2 * Hkv) * D].reshape(B, S, Hkv, D).transpose(0, 2, 1, 3)
+    q_ref = f32_to_bf16(apply_rope(q, cos, sin)).transpose(0, 2, 1, 3).reshape(B * S, H * D)
+    k_ref = f32_to_bf16(apply_rope(k, cos, sin))
+    got = host_u16(qkv)
+    assert np.array_equal(got[:, :H * D], q_ref)
+    assert np.array_equal(got[:, H * D:], rows[:, H * D:])          # k, v and padding untouched
+    kh, vh = host_u16(kc), host_u16(vt)
+    assert np.array_equal(kh[:, :, past:past + S], k_ref)
+    assert np.array_equal(vh[:, :, :, past:past + S], v.transpose(0, 1, 3, 2))
+    mask = np.ones(T_cap, bool)
+    mask[past:past + S] = False
+    assert not kh[:, :, mask].any() and not vh[:, :, :, mask].any()
+
+
+def _attn_case(rng, B, S, H, Hkv, D, past, extra_cap=0):
+    T = past + S
+    T_cap = ((T + extra_cap + 31) // 32) * 32
+    q = _bf(rng, (B * S, H * D))
+    k = _bf(rng, (B, Hkv, T_cap, D))          # finite garbage past T must be masked out
+    v = _bf(rng, (B, Hkv, T_cap, D))
+    kc = dev_bf16(k)
+    vt = dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2)))
+    cnt = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    out = _lib.attention(dev_bf16(q), B, S, H, Hkv, D, kc, vt, cnt, 1.0 / np.sqrt(D))
+    torch.cuda.synchronize()
+    rep = H // Hkv
+    q4 = bf16_to_f32(q).reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    kk = np.repeat(bf16_to_f32(k[:, :, :T]), rep, axis=1)
+    vv = np.repeat(bf16_to_f32(v[:, :, :T]), rep, axis=1)
+    ref = attention_core(q4, kk, vv, 1.0 / np.sqrt(D), T - S).transpose(0, 2, 1, 3).reshape(B * S, H * D)
+    got = bf16_to_f32(host_u16(out))
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    return err
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,D,past,extra", [
+    (1, 1, 32, 8, 128, 2047, 256),    # Llama-3-8B decode, split keys
+    (1, 1, 32, 8, 128, 0, 0),         # first position
+    (1, 1, 32, 4, 64, 150, 4000),     # TinyLlama decode, mostly empty splits
+    (16, 1, 32, 8, 128, 300, 0),      # batch-16 decode
+    (4, 1, 8, 1, 128, 1023, 0),       # 70B rank-0 shard heads, batch 4
+    (1, 1, 32, 1, 64, 70, 0),         # 32 heads on one KV head (two head groups)
+    (1, 1, 6, 6, 128, 40, 0),         # no GQA
+    (1, 64, 32, 8, 128, 0, 0),        # prefill
+    (2, 77, 8, 2, 64, 0, 5),          # ragged prefill, batch 2
+    (1, 48, 32, 8, 128, 200, 0),      # chunked prefill after a cache
+    (1, 5, 12, 4, 64, 3, 0),          # 3 heads per KV head (16 columns not filled)
+])
+def test_attention(device, B, S, H, Hkv, D, past, extra):
+    rng = np.random.default_rng(B * 7 + S * 13 + H + past)
+    err = _attn_case(rng, B, S, H, Hkv, D, past, extra)
+    print(f"attention B={B} S={S} H={H} Hkv={Hkv} D={D} past={past}: max-abs-rel {err:.2e}", flush=True)
+    assert err <= ATTN_TOL
+
+
+def test_attention_single_key_is_value(device):
+    # one cached position: softmax weight 1, output = v exactly (bf16 copy)
+    B, S, H, Hkv, D = 1, 1, 8, 2, 128
+    rng = np.random.default_rng(3)
+    q = _bf(rng, (1, H * D))
+    k = np.zeros((B, Hkv, 32, D), np.uint16)
+    v = np.zeros((B, Hkv, 32, D), np.uint16)
+    k[:, :, 0] = _bf(rng, (B, Hkv, D))
+    v[:, :, 0] = _bf(rng, (B, Hkv, D))
+    cnt = torch.tensor([0, 0], dtype=torch.int32, device="cuda")
+    out = _lib.attention(dev_bf16(q), B, S, H, Hkv, D, dev_bf16(k),
+                         dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2))), cnt, 0.1)
+    got = host_u16(out).reshape(H, D)
+    assert np.array_equal(got, np.repeat(v[0, :, 0], H // Hkv, axis=0))
+
+
+def test_attention_errors(device):
+    q = torch.zeros((1, 256), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 2, 40, 128), dtype=torch.bfloat16, device="cuda")
+    vt = torch.zeros((1, 2, 128, 40), dtype=torch.bfloat16, device="cuda")
+    cnt = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        _lib.attention(q, 1, 1, 2, 2, 128, kc, vt, cnt, 0.1)
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _lib.attention(torch.zeros((1, 192), dtype=torch.bfloat16, device="cuda"), 1, 1, 2, 2, 96,
+                       torch.zeros((1, 2, 32, 96), dtype=torch.bfloat16, device="cuda"),
+                       torch.zeros((1, 2, 96, 32), dtype=torch.bfloat16, device="cuda"), cnt, 0.1)
+
+
+@pytest.mark.parametrize("rows,I", [(1, 14336), (3, 5632), (2, 8)])
+def test_silu_mul(device, rows, I):
+    rng = np.random.default_rng(rows + I)
+    gu = _bf(rng, (rows, 2 * I), 3.0)
+    gu[0, :4] = [0x0000, 0x8000, 0x4120, 0xC120]        # 0, -0, 10, -10
+    got = host_u16(_lib.silu_mul(dev_bf16(gu)))
+    g, u = bf16_to_f32(gu[:, :I]), bf16_to_f32(gu[:, I:])
+    ref = f32_to_bf16((g / (np.float32(1) + np.exp(-g, dtype=np.float32))) * u)
+    d = bf16_ulp_diff(got, ref)
+    assert d.max() <= 1
+    assert (d > 0).mean() < 0.01
+
+
+def test_argmax(device):
+    rng = np.random.default_rng(11)
+    V = 128256
+    logits = _bf(rng, (6, V))
+    logits[1, [10, 99, 5000]] = 0x4200             # ties at the maximum: first index wins
+    logits[2, [7, 300]] = [0x7FC0, 0x7FC1]          # NaN counts as the maximum (first NaN)
+    logits[3] = 0x8000                              # all -0.0 ...
+    logits[3, 12] = 0x0000                          # ... and one +0.0: equal, index 0 wins
+    logits[4] = 0xFF80                              # -inf everywhere but one -1e30
+    logits[4, 77777] = 0xF149
+    ids = torch.empty(6, dtype=torch.int32, device="cuda")
+    tokens = torch.full((6, 4), -1, dtype=torch.int32, device="cuda")
+    step = torch.tensor([2], dtype=torch.int32, device="cuda")
+    _lib.argmax(dev_bf16(logits), ids=ids, tokens=tokens, step=step)
+    torch.cuda.synchronize()
+    ref = np.argmax(bf16_to_f32(logits), axis=-1)
+    assert np.array_equal(ids.cpu().numpy(), ref)
+    assert ref[1] == 10 and ref[2] == 7 and ref[3] == 0 and ref[4] == 77777
+    t = tokens.cpu().numpy()
+    assert np.array_equal(t[:, 2], ref) and (t[:, [0, 1, 3]] == -1).all()
+    # odd vocabulary (scalar path)
+    small = _bf(rng, (3, 1001))
+    got = _lib.argmax(dev_bf16(small)).cpu().numpy()
+    assert np.array_equal(got, np.argmax(bf16_to_f32(small), axis=-1))
+
+
+def test_add_and_counters(device):
+    rng = np.random.default_rng(5)
+    a, b = _bf(rng, (3, 4096)), _bf(rng, (3, 4096))
+    got = host_u16(_lib.add(dev_bf16(a), dev_bf16(b)))
+    assert np.array_equal(got, f32_to_bf16(bf16_to_f32(a) + bf16_to_f32(b)))
+    c = torch.tensor([5, 9, 1], dtype=torch.int32, device="cuda")
+    _lib.add_i32(c, 3, n=2)
+    _lib.add_i32(c[2:], -1, n=1)
+    assert c.cpu().tolist() == [8, 12, 0]
