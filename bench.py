@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""W4 g64 greedy decode throughput of a Llama-3-8B-shape decoder on one MI355X.
+
+Workload: random-init Llama-3-8B shape (hidden 4096, intermediate 14336, 32
+layers, 32 q / 8 kv heads of 128, vocab 128256, RoPE theta 500000, RMSNorm eps
+1e-5), every linear N(0, 0.02) quantized to MLX affine 4-bit g64 on the GPU,
+bf16 vocab embedding, W4 lm_head.  A 2048-token uniform-random prompt is
+prefilled (timed separately), then greedy decode runs as one HIP-graph replay
+per token.  A "step" is one decode token for the whole batch.
+
+Printed (one JSON line on stdout):
+* ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
+  bracketed by device synchronisation);
+* ``roofline``: the decode qGEMV (``qgemv_dma_kernel<4, 1>``): algorithmic bytes
+  (packed weights + bf16 scales and biases + x + y) per launch, averaged over the
+  129 launches of one decode step, over the average launch duration: HIP events
+  on the replay stream around graph replays of exactly those launches (a graph
+  runs them back to back, so the average is the kernels' own), against 8 TB/s;
+  ``traffic`` is the measured HBM bytes per launch recorded under ``profiles/``
+  (null when absent);
+* ``cpu_baseline``: the C restatement of the quantized matmul (OpenMP, fp64
+  accumulation) timed on this host on a bounded sample: decoder layer 0's four
+  projections plus 1/32 of the lm_head rows at M = batch, repeated for ~10 s,
+  scaled to tokens/s of the 32-layer model's linear layers.
+"""
+import argparse
+import asyncio
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "W4 decode tok/s (Llama-3-8B shape, bs1) + qGEMV HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_dma_w4_llama3_8b_decode_traffic.json")
+
+LLAMA3_8B = dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv_heads=8, theta=500000.0, eps=1e-5)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=128, help="timed decode steps")
+    p.add_argument("--warmup", type=int, default=16, help="untimed decode steps")
+    p.add_argument("--batch", type=int, default=1)
+    p.add_argument("--prefill", type=int, default=2048)
+    p.add_argument("--layers", type=int, default=LLAMA3_8B["layers"])
+    p.add_argument("--bits", type=int, default=4, choices=(4, 8))
+    p.add_argument("--kernel-reps", type=int, default=5, help="graph replays of the per-launch GEMV timing")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--kernels-only", action="store_true",
+                   help="build the weights and run only the per-launch GEMV pass (for counter profiling)")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------- model
+
+
+def build_model(cfg, layers, bits, capacity, seed=0):
+    import torch
+    from shardcompute_amd import _lib
+    from shardcompute_amd.parallel.transformer import ParallelTransformer
+    dev = torch.device("cuda", 0)
+    H, I, V = cfg["hidden"], cfg["inter"], cfg["vocab"]
+    D = H // cfg["heads"]
+    nq, nkv = cfg["heads"] * D, cfg["kv_heads"] * D
+    m = ParallelTransformer(vocab_size=V, hidden_size=H, num_layers=layers, num_heads=cfg["heads"],
+                            intermediate_size=I, world_size=1, rank=0, num_kv_heads=cfg["kv_heads"],
+                            max_position_embeddings=capacity, rms_norm_eps=cfg["eps"], rope_base=cfg["theta"],
+                            use_quantized=True, quantization_bits=bits, quantization_group_size=64,
+                            embedding="vocab", quantized_lm_head=True, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def q(n, k):
+        w = torch.randn((n, k), generator=g, device=dev, dtype=torch.float32).mul_(0.02)
+        out = _lib.quantize(w, bits=bits)
+        del w
+        return out
+
+    def norm_w():
+        return (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+
+    for layer in m.layers:
+        layer.input_layernorm.load_weights(norm_w())
+        layer.post_attention_layernorm.load_weights(norm_w())
+        wq, s, b = q(nq + 2 * nkv, H)
+        o = q(H, nq)
+        sl = [slice(0, nq), slice(nq, nq + nkv), slice(nq + nkv, nq + 2 * nkv)]
+        layer.attention.load_quantized_shards(wq[sl[0]], s[sl[0]], b[sl[0]], None, wq[sl[1]], s[sl[1]], b[sl[1]],
+                                              None, wq[sl[2]], s[sl[2]], b[sl[2]], None, *o, None)
+        gwq, gs, gb = q(2 * I, H)
+        d = q(H, I)
+        layer.mlp.load_quantized_shards(gwq[I:], gs[I:], gb[I:], None, *d, None, gwq[:I], gs[:I], gb[:I], None)
+        del wq, s, b, gwq, gs, gb
+    emb = torch.randn((V, H), generator=g, device=dev, dtype=torch.float32).mul_(0.02).to(torch.bfloat16)
+    m.load_embedding_weights(emb)
+    m.load_norm_weights(norm_w())
+    m.load_quantized_lm_head_weights(*q(V, H))
+    # build the fused q|k|v and gate|up matrices now (outside any timed region)
+    for layer in m.layers:
+        layer.attention.qkv.build()
+        layer.mlp.gate_up.build()
+    torch.cuda.synchronize()
+    return m
+
+
+def gemv_launches(model):
+    """(name, wq, scales, biases, K, N) of every quantized product of one decode step."""
+    out = []
+    for i, layer in enumerate(model.layers):
+        att, mlp = layer.attention, layer.mlp
+        qkv, gu = att.qkv, mlp.gate_up
+        K = model.hidden_size
+        out.append(("qkv", qkv._wq, qkv._s, qkv._b, K, qkv.out_features))
+        op = att.o_proj
+        out.append(("o", op.quantized_weight, op.scales, op.biases_quant, op.local_in_features, op.out_features))
+        out.append(("gate_up", gu._wq, gu._s, gu._b, K, gu.out_features))
+        dp = mlp.down_proj
+        out.append(("down", dp.quantized_weight, dp.scales, dp.biases_quant, dp.local_in_features, dp.out_features))
+    lm = model.lm_head
+    out.append(("lm_head", lm.quantized_weight, lm.scales, lm.biases_quant, model.hidden_size,
+                lm.local_out_features))
+    return out
+
+
+def qmm_bytes(M, N, K, bits):
+    """Algorithmic bytes of one quantized product: weights + bf16 scales/biases + x + y."""
+    return N * K * bits // 8 + N * (K // 64) * 2 * 2 + M * K * 2 + M * N * 2
+
+
+def _gemv_io(launches, batch):
+    import torch
+    dev = torch.device("cuda", 0)
+    xs = {K: torch.randn((batch, K), device=dev).to(torch.bfloat16) for K in {l[4] for l in launches}}
+    ys = {N: torch.empty((batch, N), dtype=torch.bfloat16, device=dev) for N in {l[5] for l in launches}}
+    return xs, ys
+
+
+def _launch_all(launches, xs, ys, bits):
+    from shardcompute_amd import _lib
+    for name, wq, s, b, K, N in launches:
+        _lib.qmm(xs[K], wq, s, b, bits=bits, out=ys[N])
+
+
+def time_gemv_launches(model, batch, bits, reps):
+    """Average duration of the decode step's quantized-product launches.
+
+    The launches of one step (every layer's q|k|v, o, gate|up, down and the
+    lm_head, on the model's own weights: 4.2 GB, far beyond the 256 MB
+    last-level cache) are captured in a HIP graph, which runs them back to back
+    with no host gaps; HIP events on the replay stream bracket ``reps`` replays.
+    The same is done per projection kind for the per-shape breakdown."""
+    import torch
+    launches = gemv_launches(model)
+    xs, ys = _gemv_io(launches, batch)
+
+    def graph_of(ls):
+        _launch_all(ls, xs, ys, bits)          # warm (kernel attributes set outside capture)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            _launch_all(ls, xs, ys, bits)
+        return g
+
+    def timed(g, n_launch):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * n_launch)
+
+    avg_us = timed(graph_of(launches), len(launches))
+    tot_bytes = sum(qmm_bytes(batch, l[5], l[4], bits) for l in launches)
+    per = {}
+    for kind in ("qkv", "o", "gate_up", "down", "lm_head"):
+        ls = [l for l in launches if l[0] == kind]
+        us = timed(graph_of(ls), len(ls))
+        nb = qmm_bytes(batch, ls[0][5], ls[0][4], bits)
+        per[kind] = {"K": ls[0][4], "N": ls[0][5], "avg_us": round(us, 3), "GBs": round(nb / (us * 1e-6) / 1e9, 1)}
+    bpl = tot_bytes / len(launches)
+    log(f"gemv: {len(launches)} launches/step, avg {avg_us:.3f} us, {bpl / 1e6:.2f} MB/launch, "
+        f"{bpl / (avg_us * 1e-6) / 1e9:.0f} GB/s")
+    return dict(avg_us=avg_us, bytes_per_launch=bpl, GBs=bpl / (avg_us * 1e-6) / 1e9,
+                launches_per_step=len(launches), per_shape=per)
+
+
+def eager_gemv_passes(model, batch, bits, passes):
+    """The same launches, eager (for hardware-counter runs, one dispatch at a time)."""
+    import torch
+    launches = gemv_launches(model)
+    xs, ys = _gemv_io(launches, batch)
+    for _ in range(passes):
+        _launch_all(launches, xs, ys, bits)
+    torch.cuda.synchronize()
+    return launches
+
+
+# ---------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(model, batch, bits, seconds):
+    """The C restatement on decoder layer 0's projections + 1/32 of the lm_head rows."""
+    import numpy as np
+    import torch
+    from oracle import cref
+
+    def u32(t):
+        return t.cpu().view(torch.int32).numpy().view(np.uint32)
+
+    def u16(t):
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+    if not cref.available():
+        cref.build()
+    threads = cref.default_threads()
+    launches = gemv_launches(model)
+    layer0 = launches[:4]
+    name, lwq, ls, lb, K, N = launches[-1]
+    rows = N // 32
+    sample = [(u32(l[1]), u16(l[2]), u16(l[3]), l[4]) for l in layer0]
+    lm = (u32(lwq[:rows]), u16(ls[:rows]), u16(lb[:rows]), K)
+    rng = np.random.default_rng(0)
+    xs = {k: (rng.standard_normal((batch, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+          for k in {s[3] for s in sample}}
+    reps, t_layer, t_lm = 0, 0.0, 0.0
+    t_start = time.perf_counter()
+    while reps == 0 or (time.perf_counter() - t_start) < seconds:
+        t0 = time.perf_counter()
+        for wq, s, b, k in sample:
+            cref.qmm_bf16(xs[k], wq, s, b, bits=bits, threads=threads)
+        t1 = time.perf_counter()
+        cref.qmm_bf16(xs[lm[3]], lm[0], lm[1], lm[2], bits=bits, threads=threads)
+        t2 = time.perf_counter()
+        t_layer += t1 - t0
+        t_lm += t2 - t1
+        reps += 1
+    per_token = model.num_layers * t_layer / reps + 32 * t_lm / reps
+    return {"value": round(batch / per_token, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": (f"oracle C restatement (fp64 accumulate, OpenMP) of the W{bits} g64 quantized matmuls: "
+                       f"decoder layer 0's q|k|v, o, gate|up, down plus lm_head rows [0, {rows}) at M={batch}, "
+                       f"{reps} repetitions in {time.perf_counter() - t_start:.1f} s, scaled x{model.num_layers} "
+                       f"layers and x32 lm_head rows; attention and norms not included")}
+
+
+# ---------------------------------------------------------------- main
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        log(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
+            f"(no collectives; the multi-GPU sharding is a design note only)")
+        sys.exit(2)
+    import torch
+    from shardcompute_amd import _lib
+    from shardcompute_amd.executor import DecodeGraph
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        sys.exit(1)
+    _lib.load()
+    cfg = dict(LLAMA3_8B)
+    B, P, K, W = args.batch, args.prefill, args.steps, args.warmup
+    capacity = P + W + K + 8
+    t_build = time.perf_counter()
+    model = build_model(cfg, args.layers, args.bits, capacity)
+    log(f"built {args.layers}-layer W{args.bits} model in {time.perf_counter() - t_build:.1f} s "
+        f"({torch.cuda.memory_allocated() / 2**30:.2f} GiB allocated)")
+
+    if args.kernels_only:
+        # a plain copy of known size first (256 MiB read + 256 MiB written), to scale
+        # the HBM counters, then the decode step's quantized products, eager
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        ls = eager_gemv_passes(model, B, args.bits, args.kernel_reps)
+        log(f"kernels-only: 3 copies of {src.numel()} bytes, {args.kernel_reps} x {len(ls)} quantized products")
+        return
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1)
+    ids = torch.randint(0, cfg["vocab"], (B, P), generator=gen, device="cuda", dtype=torch.int64)
+    cache = model.new_cache(B, capacity)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits, _ = asyncio.run(model.forward(ids, past_key_values=cache, use_cache=True, last_only=True))
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"prefill {P} tokens x {B}: {prefill_s * 1e3:.1f} ms")
+
+    tokens = torch.zeros((B, W + K + 2), dtype=torch.int32, device="cuda")
+    dec = DecodeGraph(model, cache, tokens)
+    _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
+    _lib.add_i32(cache.counters[1:], 1, n=1)
+    dec.run(1)            # eager step, then capture
+    dec.run(W)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.run(K)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    tok_s = B * K / el
+    ms_step = el / K * 1e3
+    log(f"decode: {K} steps in {el * 1e3:.1f} ms -> {ms_step:.3f} ms/step, {tok_s:.1f} tok/s")
+    first = tokens[0, :8].tolist()
+
+    g = time_gemv_launches(model, B, args.bits, args.kernel_reps)
+    step_gemv_bytes = g["bytes_per_launch"] * g["launches_per_step"]
+    step_gemv_ms = g["avg_us"] * g["launches_per_step"] / 1e3
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roof = {"bound": "hbm", "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": f"qgemv_dma_kernel<{args.bits}, 1>" if B == 1 else "qgemv",
+            "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
+            "launches_per_step": g["launches_per_step"]}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        try:
+            cpu = cpu_baseline(model, B, args.bits, args.cpu_seconds)
+        except Exception as e:       # the baseline is reported, never required
+            log(f"cpu baseline unavailable: {e}")
+
+    kv_bytes = 2 * args.layers * B * cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"]) * 2 * (P + W + K // 2)
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic: random-init N(0,0.02) weights quantized W4 g64 on the GPU, "
+                                 "uniform random prompt ids",
+        "config": {"workload": f"Llama-3-8B-shape W{args.bits}g64 greedy decode, batch {B}, after a {P}-token "
+                               f"prefill", "batch": B, "prefill_tokens": P, "layers": args.layers,
+                   "hidden": cfg["hidden"], "intermediate": cfg["inter"], "heads": cfg["heads"],
+                   "kv_heads": cfg["kv_heads"], "vocab": cfg["vocab"], "weights": f"W{args.bits} g64, bf16 s/b",
+                   "activations": "bf16, fp32 accumulate", "decode": "HIP graph replay per token"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "prefill": {"tokens": B * P, "ms": round(prefill_s * 1e3, 2), "tok_s": round(B * P / prefill_s, 1)},
+        "decode_step": {"gemv_ms": round(step_gemv_ms, 4), "gemv_bytes": int(step_gemv_bytes),
+                        "kv_bytes_avg": int(kv_bytes),
+                        "step_hbm_frac": round((step_gemv_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9
+                                               / HBM_PEAK_GBS, 4)},
+        "gemv_per_shape": g["per_shape"],
+        "first_tokens": first,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -65,12 +65,18 @@ __device__ __forceinline__ uint4 perm_w4x(uint4 v) {
 }
 
 // 16 bytes per active lane from global `g` to LDS byte address lds_base + 16 * lane.
+// The instruction takes its LDS base from M0, which this block sets itself; the
+// kernel has no other M0 user (no LDS-DMA builtins, no indirect register access),
+// so declaring the clobber is all the compiler needs (it warns regardless).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                  :
                  : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
                  : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // (x & mask) | magic.  VOP3 on gfx950 takes no literal and one scalar operand, so
 // with both constants as literals the compiler emits and + or; with the mask in an
@@ -143,7 +149,6 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
 
     const int lo = (int)(((long)wave * items) / nwaves);
     const int hi = (int)(((long)(wave + 1) * items) / nwaves);
-    const int last = hi > lo ? hi - 1 : 0;
 
     // ---- item DMA: 4 x (4 rows x 256 B, row-rotated) + scales/biases of the 16 rows.
     // Pointers advance incrementally; they are rebuilt only when the tile changes.
