@@ -126,44 +126,46 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
 // cache-less calls such as forward_sync_partial(position_offset=...)).
 // q and k heads are rotated with the rotate-half rule x*cos + [-x2, x1]*sin
 // (attention.py:130-151) using fp32 tables; rotated q is written back in place,
-// rotated k and the raw v go to the cache.  One workgroup per token.
+// rotated k and the raw v go to the cache.
 __global__ void __launch_bounds__(256)
 rope_append_kernel(uint16_t *__restrict__ qkv, long qkv_stride, int S, int H, int Hkv, int D,
                    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
                    uint16_t *__restrict__ kc, uint16_t *__restrict__ vt, int T_cap,
                    const int32_t *__restrict__ cache_len, int pos_offset, int table_len) {
-#pragma clang fp contract(off)
+    // one wave per head of one token: q heads, then k heads, then v heads
     const int tok = blockIdx.x;
+    const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (head >= H + 2 * Hkv) return;
     const int b = tok / S, s = tok - (tok / S) * S;
     const int pos = cache_len[0] + s;             // cache slot
     const int rpos = pos + pos_offset;            // rotary position
     // the host sizes cache and tables for every launch; a counter that has run past
     // them (a stale replay) leaves the cache untouched instead of writing out of bounds
     if (pos < 0 || pos >= T_cap || rpos < 0 || rpos >= table_len) return;
-    uint16_t *row = qkv + (size_t)tok * qkv_stride;
+    uint16_t *hp = qkv + (size_t)tok * qkv_stride + (size_t)head * D;
     const int half = D >> 1;
-    const float *ct = cos_t + (size_t)rpos * half;
-    const float *st = sin_t + (size_t)rpos * half;
-    for (int idx = threadIdx.x; idx < (H + Hkv) * half; idx += blockDim.x) {
-        const int head = idx / half, i = idx - (idx / half) * half;
-        uint16_t *hp = row + (size_t)head * D;
-        const float x1 = bf2f(hp[i]), x2 = bf2f(hp[i + half]);
-        const float c = ct[i], sn = st[i];
-        const uint16_t o1 = (uint16_t)f2bf(add_rn(mul_rn(x1, c), mul_rn(-x2, sn)));
-        const uint16_t o2 = (uint16_t)f2bf(add_rn(mul_rn(x2, c), mul_rn(x1, sn)));
-        if (head < H) {
-            hp[i] = o1;
-            hp[i + half] = o2;
-        } else {
-            uint16_t *kr = kc + (((size_t)b * Hkv + (head - H)) * T_cap + pos) * D;
-            kr[i] = o1;
-            kr[i + half] = o2;
+    if (head < H + Hkv) {
+        const float *ct = cos_t + (size_t)rpos * half;
+        const float *st = sin_t + (size_t)rpos * half;
+        uint16_t *kr = kc + (((size_t)b * Hkv + (head - H)) * T_cap + pos) * D;
+        for (int i = lane; i < half; i += 64) {
+            const float x1 = bf2f(hp[i]), x2 = bf2f(hp[i + half]);
+            const float c = ct[i], sn = st[i];
+            const uint16_t o1 = (uint16_t)f2bf(add_rn(mul_rn(x1, c), mul_rn(-x2, sn)));
+            const uint16_t o2 = (uint16_t)f2bf(add_rn(mul_rn(x2, c), mul_rn(x1, sn)));
+            if (head < H) {
+                hp[i] = o1;
+                hp[i + half] = o2;
+            } else {
+                kr[i] = o1;
+                kr[i + half] = o2;
+            }
         }
-    }
-    const uint16_t *vr = row + (size_t)(H + Hkv) * D;
-    for (int idx = threadIdx.x; idx < Hkv * D; idx += blockDim.x) {
-        const int hk = idx / D, d = idx - (idx / D) * D;
-        vt[(((size_t)b * Hkv + hk) * D + d) * T_cap + pos] = vr[idx];
+    } else {
+        const int hk = head - H - Hkv;
+        uint16_t *vc = vt + ((size_t)b * Hkv + hk) * D * T_cap + pos;
+        for (int d = lane; d < D; d += 64) vc[(size_t)d * T_cap] = hp[d];
     }
 }
 
@@ -190,7 +192,7 @@ struct AttnArgs {
     const int32_t *cache_len; // positions cached before this call's S new ones
     uint16_t *out;
     long out_stride;
-    float *part;             // [B, H, S, nsplit, D + 2] when nsplit > 1
+    float *part;             // [B, H, S, nsplit, D + 4] when nsplit > 1: o[D], m, l, pad
     int B, S, H, Hkv, T_cap;
     int R, Rc, Pw, hgroups, npb;
     int kps, nsplit;
@@ -198,17 +200,90 @@ struct AttnArgs {
 };
 
 constexpr int ATTN_WAVES = 4;
+constexpr int ATTN_KB = 32;                       // keys per block
+constexpr int ATTN_STRIDE = ATTN_WAVES * ATTN_KB;  // a workgroup's waves take interleaved blocks
+
+// One key block's operands, loaded together: K rows for S^T (two 16-key tiles x
+// D/32 k-steps) and Vt rows for O^T (D/16 tiles x keys {4g..4g+3, 16+4g..16+4g+3}).
+template <int D>
+struct AttnBlock {
+    uint4 k[2][D / 32];
+    uint2 v[D / 16][2];
+};
 
 template <int D>
+__device__ __forceinline__ void attn_load(AttnBlock<D> &blk, const uint16_t *kbase, const uint16_t *vbase, int T_cap,
+                                          int kb, int c, int g) {
+#pragma unroll
+    for (int u = 0; u < D / 32; ++u) {
+        blk.k[0][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + c) * D + 32 * u + 8 * g);
+        blk.k[1][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + 16 + c) * D + 32 * u + 8 * g);
+    }
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+        const uint16_t *vr = vbase + (size_t)(16 * n + c) * T_cap + kb + 4 * g;
+        blk.v[n][0] = *reinterpret_cast<const uint2 *>(vr);
+        blk.v[n][1] = *reinterpret_cast<const uint2 *>(vr + 16);
+    }
+}
+
+// S^T, masked online softmax and O^T update for one block of 32 keys.
+template <int D>
+__device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8_t *qv, int kb, int limit, int g,
+                                           float scale_log2, float &m, float &lsum, f4 *o) {
+    f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < D / 32; ++u) {
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(blk.k[0][u]), qv[u], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(blk.k[1][u]), qv[u], s1, 0, 0, 0);
+    }
+    float sv[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        sv[r] = (kb + 4 * g + r <= limit) ? s0[r] * scale_log2 : -INFINITY;
+        sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * scale_log2 : -INFINITY;
+    }
+    float bm = sv[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) bm = fmaxf(bm, sv[r]);
+    bm = fmaxf(bm, __shfl_xor(bm, 16));
+    bm = fmaxf(bm, __shfl_xor(bm, 32));
+    const float mn = fmaxf(m, bm);
+    const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
+    float p[8], ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        p[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - mn);
+        ps += p[r];
+    }
+    lsum = lsum * alpha + ps;
+    m = mn;
+    const bf16x8_t pb8 = as_bf16x8(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
+                                   pack_bf16x2(p[6], p[7]));
+#pragma unroll
+    for (int n = 0; n < D / 16; ++n) {
+        f4 acc = o[n];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] *= alpha;
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(blk.v[n][0].x, blk.v[n][0].y, blk.v[n][1].x, blk.v[n][1].y), pb8, acc, 0, 0, 0);
+    }
+}
+
+// A workgroup owns 16 columns and one key range [k_lo, k_hi); its 4 waves take the
+// range's 32-key blocks round-robin (next block prefetched while one is computed),
+// then merge their (m, l, O) through LDS.  With one key range the merged result is
+// the output; with several it is a partial for attn_combine_kernel.
+template <int D>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
-    constexpr int U = D / 32;    // k-steps of S^T
-    constexpr int DT = D / 16;   // 16-row tiles of O^T
+    constexpr int U = D / 32;
+    constexpr int DT = D / 16;
+    __shared__ float sm_m[ATTN_WAVES][16], sm_l[ATTN_WAVES][16];
+    __shared__ float sm_o[ATTN_WAVES][D][17];
     const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const long wid = (long)blockIdx.x * ATTN_WAVES + (threadIdx.x >> 6);
-    const long total = (long)a.B * a.Hkv * a.hgroups * a.npb * a.nsplit;
-    if (wid >= total) return;
-    long t = wid;
+    long t = blockIdx.x;
     const int sp = (int)(t % a.nsplit); t /= a.nsplit;
     const int pb = (int)(t % a.npb); t /= a.npb;
     const int hg = (int)(t % a.hgroups); t /= a.hgroups;
@@ -217,16 +292,21 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
 
     const int T = a.cache_len[0] + a.S;   // cached positions, the S new ones included
     const int off = T - a.S;
-    const int hr = hg * 16 + (c % a.Rc);
-    const int pos = pb * a.Pw + c / a.Rc;
-    const bool col_ok = (c < a.Pw * a.Rc) && (hr < a.R) && (pos < a.S);
-    const int h = hk * a.R + hr;
-    const int limit = col_ok ? min(pos + off, T - 1) : -1;   // last key this column may see
     const int maxpos = min(pb * a.Pw + a.Pw - 1, a.S - 1);
     const int k_lo = sp * a.kps;
     const int k_hi = min(min(k_lo + a.kps, T), maxpos + off + 1);
+    if (k_lo >= T) return;   // a range wholly past the cache: the combine never reads it
 
-    // Q^T operand: column c, dims 32u + 8g .. +7
+    auto col_info = [&](int cc, int &pos, int &h) {
+        const int hr = hg * 16 + (cc % a.Rc);
+        pos = pb * a.Pw + cc / a.Rc;
+        h = hk * a.R + hr;
+        return (cc < a.Pw * a.Rc) && (hr < a.R) && (pos < a.S);
+    };
+    int pos, h;
+    const bool col_ok = col_info(c, pos, h);
+    const int limit = col_ok ? min(pos + off, T - 1) : -1;   // last key this column may see
+
     bf16x8_t qv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -243,95 +323,116 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int n = 0; n < DT; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = k_lo; kb < k_hi; kb += 32) {
-        f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint4 k0 = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + c) * D + 32 * u + 8 * g);
-            const uint4 k1 = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + 16 + c) * D + 32 * u + 8 * g);
-            s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k0), qv[u], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k1), qv[u], s1, 0, 0, 0);
-        }
-        float sv[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            sv[r] = (kb + 4 * g + r <= limit) ? s0[r] * a.scale_log2 : -INFINITY;
-            sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * a.scale_log2 : -INFINITY;
-        }
-        float bm = sv[0];
-#pragma unroll
-        for (int r = 1; r < 8; ++r) bm = fmaxf(bm, sv[r]);
-        bm = fmaxf(bm, __shfl_xor(bm, 16));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
-        const float mn = fmaxf(m, bm);
-        const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
-        float p[8], ps = 0.f;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            p[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - mn);
-            ps += p[r];
-        }
-        lsum = lsum * alpha + ps;
-        m = mn;
-        const bf16x8_t pb8 = as_bf16x8(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                                       pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7]));
-#pragma unroll
-        for (int n = 0; n < DT; ++n) {
-            const uint16_t *vr = vbase + (size_t)(16 * n + c) * a.T_cap + kb + 4 * g;
-            const uint2 v0 = *reinterpret_cast<const uint2 *>(vr);
-            const uint2 v1 = *reinterpret_cast<const uint2 *>(vr + 16);
-            f4 acc = o[n];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] *= alpha;
-            o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v0.x, v0.y, v1.x, v1.y), pb8, acc, 0, 0, 0);
-        }
+    // Loads are unconditional (a wave past its range reloads its current block, an
+    // L1/L2 hit): a load issued only on some paths makes the compiler wait for every
+    // outstanding load, the prefetch included, before the current block's compute.
+    AttnBlock<D> cur, nxt;
+    const int clampk = a.T_cap - ATTN_KB;
+    int kb = k_lo + ATTN_KB * w;
+    attn_load<D>(cur, kbase, vbase, a.T_cap, min(kb, clampk), c, g);
+    while (true) {
+        const int kn = kb + ATTN_STRIDE;
+        attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
+        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+        if (kn >= k_hi) break;
+        const int kn2 = kn + ATTN_STRIDE;
+        attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
+        attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
+        if (kn2 >= k_hi) break;
+        kb = kn2;
     }
     float ltot = lsum + __shfl_xor(lsum, 16);
     ltot += __shfl_xor(ltot, 32);
-    if (!col_ok) return;
-    if (a.nsplit == 1) {
-        const float inv = 1.f / ltot;
-        uint16_t *orow = a.out + ((size_t)b * a.S + pos) * a.out_stride + (size_t)h * D;
+
+    // ---- merge the 4 waves: o[n][r] is O^T[dim 16n + 4g + r][column c]
+    if (g == 0) {
+        sm_m[w][c] = m;
+        sm_l[w][c] = ltot;
+    }
 #pragma unroll
-        for (int n = 0; n < DT; ++n) {
-            uint2 v;
-            v.x = pack_bf16x2(o[n][0] * inv, o[n][1] * inv);
-            v.y = pack_bf16x2(o[n][2] * inv, o[n][3] * inv);
-            *reinterpret_cast<uint2 *>(orow + 16 * n + 4 * g) = v;
+    for (int n = 0; n < DT; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm_o[w][16 * n + 4 * g + r][c] = o[n][r];
+    __syncthreads();
+    const int cc = threadIdx.x & 15;
+    int cpos, ch;
+    if (!col_info(cc, cpos, ch)) return;
+    float M = sm_m[0][cc];
+#pragma unroll
+    for (int i = 1; i < ATTN_WAVES; ++i) M = fmaxf(M, sm_m[i][cc]);
+    float wt[ATTN_WAVES], L = 0.f;
+#pragma unroll
+    for (int i = 0; i < ATTN_WAVES; ++i) {
+        wt[i] = (sm_m[i][cc] == -INFINITY) ? 0.f : exp2f(sm_m[i][cc] - M);
+        L += wt[i] * sm_l[i][cc];
+    }
+    constexpr int PER = D * 16 / (64 * ATTN_WAVES);      // dims per thread
+    const int d0 = threadIdx.x >> 4;                     // 0..15
+    if (a.nsplit == 1) {
+        const float inv = 1.f / L;
+        uint16_t *orow = a.out + ((size_t)b * a.S + cpos) * a.out_stride + (size_t)ch * D;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int d = d0 + 16 * j;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ATTN_WAVES; ++i) acc += wt[i] * sm_o[i][d][cc];
+            orow[d] = (uint16_t)f2bf(acc * inv);
         }
     } else {
-        float *pp = a.part + ((((size_t)b * a.H + h) * a.S + pos) * a.nsplit + sp) * (D + 4);
+        float *pp = a.part + ((((size_t)b * a.H + ch) * a.S + cpos) * a.nsplit + sp) * (D + 4);
 #pragma unroll
-        for (int n = 0; n < DT; ++n)
-            *reinterpret_cast<float4 *>(pp + 16 * n + 4 * g) = make_float4(o[n][0], o[n][1], o[n][2], o[n][3]);
-        if (g == 0) {
-            pp[D] = m;
-            pp[D + 1] = ltot;
+        for (int j = 0; j < PER; ++j) {
+            const int d = d0 + 16 * j;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ATTN_WAVES; ++i) acc += wt[i] * sm_o[i][d][cc];
+            pp[d] = acc;
+        }
+        if (d0 == 0) {
+            pp[D] = M;
+            pp[D + 1] = L;
         }
     }
 }
 
-// Merges the key-split partials of one (b, h, position) per wave.
+// Merges the key-range partials of one (b, h, position) per wave: lane i holds
+// partial i's (m, l); each lane then sums dims lane, lane + 64 over the partials.
 template <int D>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     const long wid = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (wid >= (long)a.B * a.H * a.S) return;
     const int T = a.cache_len[0] + a.S;
-    const int used = min(a.nsplit, (T + a.kps - 1) / a.kps);
+    const int used = min(a.nsplit, (T + a.kps - 1) / a.kps);   // <= 64 by construction
     const float *pp = a.part + wid * a.nsplit * (D + 4);
-    float M = -INFINITY;
-    for (int i = 0; i < used; ++i) M = fmaxf(M, pp[(size_t)i * (D + 4) + D]);
+    const float mi = lane < used ? pp[(size_t)lane * (D + 4) + D] : -INFINITY;
+    const float li = lane < used ? pp[(size_t)lane * (D + 4) + D + 1] : 0.f;
+    float M = mi;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float wi = (mi == -INFINITY) ? 0.f : exp2f(mi - M);
+    const float L = wave_sum(wi * li);
     constexpr int PER = D / 64;
     float acc[PER] = {};
-    float L = 0.f;
-    for (int i = 0; i < used; ++i) {
-        const float *pi = pp + (size_t)i * (D + 4);
-        const float mi = pi[D];
-        const float wgt = (mi == -INFINITY) ? 0.f : exp2f(mi - M);
-        L += wgt * pi[D + 1];
+    int i = 0;
+    for (; i + 4 <= used; i += 4) {
+        float v[4][PER];
 #pragma unroll
-        for (int e = 0; e < PER; ++e) acc[e] += wgt * pi[lane + 64 * e];
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int e = 0; e < PER; ++e) v[k][e] = pp[(size_t)(i + k) * (D + 4) + lane + 64 * e];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float wk = __shfl(wi, i + k);
+#pragma unroll
+            for (int e = 0; e < PER; ++e) acc[e] += wk * v[k][e];
+        }
+    }
+    for (; i < used; ++i) {
+        const float wk = __shfl(wi, i);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[e] += wk * pp[(size_t)i * (D + 4) + lane + 64 * e];
     }
     const int bh = (int)(wid / a.S), pos = (int)(wid % a.S);
     const int b = bh / a.H, h = bh % a.H;
@@ -456,7 +557,7 @@ namespace {
 
 struct AttnPlan {
     AttnArgs a;
-    long waves;
+    long blocks;
 };
 
 void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPlan *pl) {
@@ -468,13 +569,17 @@ void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPl
     a.hgroups = (a.R + 15) / 16;
     a.npb = (int)((S + a.Pw - 1) / a.Pw);
     const long base = B * Hkv * a.hgroups * a.npb;
-    // split the keys when the (batch, head, position) waves alone cannot fill the GPU
-    const long target = 4L * device_info().num_cus;
+    // split the keys into ranges when the (batch, head, position) workgroups alone
+    // cannot fill the GPU; a range covers one block per wave at least, and at most
+    // 64 ranges are merged (one per lane of the combine)
+    const long target = 2L * device_info().num_cus;
     int nsplit = 1;
-    if (base < target) {
+    if (base < target && T_cap > ATTN_STRIDE) {
         long want = (target + base - 1) / base;
         long kps = (T_cap + want - 1) / want;
-        kps = ((kps + 63) / 64) * 64;   // at least two key blocks per wave
+        kps = ((kps + ATTN_STRIDE - 1) / ATTN_STRIDE) * ATTN_STRIDE;
+        long cap64 = ((T_cap + 63) / 64 + ATTN_STRIDE - 1) / ATTN_STRIDE * ATTN_STRIDE;
+        if (kps < cap64) kps = cap64;
         nsplit = (int)((T_cap + kps - 1) / kps);
         a.kps = (int)kps;
     }
@@ -483,7 +588,7 @@ void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPl
         a.kps = (int)T_cap;
     }
     a.nsplit = nsplit;
-    pl->waves = base * nsplit;
+    pl->blocks = base * nsplit;
 }
 
 }  // namespace
@@ -513,7 +618,8 @@ int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, l
     if (T_cap <= 0 || table_len <= 0 || pos_offset < 0 || T_cap > 0x7FFFFFFFL || table_len > 0x7FFFFFFFL ||
         pos_offset > 0x7FFFFFFFL)
         return set_error(SC_EINVAL, "rope_append: bad capacity/table/offset");
-    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(B * S)), dim3(256), 0, stream, qkv, qkv_stride, (int)S,
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(B * S), (unsigned)((H + 2 * Hkv + 3) / 4)), dim3(256), 0,
+                       stream, qkv, qkv_stride, (int)S,
                        (int)H, (int)Hkv, (int)D, cos_t, sin_t, kc, vt, (int)T_cap, cache_len, (int)pos_offset,
                        (int)table_len);
     SC_HIP_CHECK(hipGetLastError());
@@ -554,7 +660,7 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
         if ((uintptr_t)workspace % 16) return set_error(SC_EINVAL, "attention: workspace must be 16-byte aligned");
         a.part = static_cast<float *>(workspace);
     }
-    const unsigned blocks = (unsigned)((pl.waves + ATTN_WAVES - 1) / ATTN_WAVES);
+    const unsigned blocks = (unsigned)pl.blocks;
     if (D == 128) hipLaunchKernelGGL(attn_kernel<128>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
     else hipLaunchKernelGGL(attn_kernel<64>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
     SC_HIP_CHECK(hipGetLastError());
