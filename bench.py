@@ -115,20 +115,24 @@ def build_model(cfg, layers, bits, capacity, seed=0):
 
 
 def gemv_launches(model):
-    """(name, wq, scales, biases, K, N) of every quantized product of one decode step."""
+    """(name, prologue, wq, scales, biases, K, N) of every quantized product of one
+    decode step, with the input transformation its kernel applies: "norm" (RMSNorm
+    + residual add) or "" (plain)."""
     out = []
-    for i, layer in enumerate(model.layers):
+    for layer in model.layers:
         att, mlp = layer.attention, layer.mlp
         qkv, gu = att.qkv, mlp.gate_up
         K = model.hidden_size
-        out.append(("qkv", qkv._wq, qkv._s, qkv._b, K, qkv.out_features))
+        out.append(("qkv", "norm", qkv._wq, qkv._s, qkv._b, K, qkv.out_features))
         op = att.o_proj
-        out.append(("o", op.quantized_weight, op.scales, op.biases_quant, op.local_in_features, op.out_features))
-        out.append(("gate_up", gu._wq, gu._s, gu._b, K, gu.out_features))
+        out.append(("o", "", op.quantized_weight, op.scales, op.biases_quant, op.local_in_features,
+                    op.out_features))
+        out.append(("gate_up", "norm", gu._wq, gu._s, gu._b, K, gu.out_features))
         dp = mlp.down_proj
-        out.append(("down", dp.quantized_weight, dp.scales, dp.biases_quant, dp.local_in_features, dp.out_features))
+        out.append(("down", "", dp.quantized_weight, dp.scales, dp.biases_quant, dp.local_in_features,
+                    dp.out_features))
     lm = model.lm_head
-    out.append(("lm_head", lm.quantized_weight, lm.scales, lm.biases_quant, model.hidden_size,
+    out.append(("lm_head", "norm", lm.quantized_weight, lm.scales, lm.biases_quant, model.hidden_size,
                 lm.local_out_features))
     return out
 
@@ -141,15 +145,25 @@ def qmm_bytes(M, N, K, bits):
 def _gemv_io(launches, batch):
     import torch
     dev = torch.device("cuda", 0)
-    xs = {K: torch.randn((batch, K), device=dev).to(torch.bfloat16) for K in {l[4] for l in launches}}
-    ys = {N: torch.empty((batch, N), dtype=torch.bfloat16, device=dev) for N in {l[5] for l in launches}}
-    return xs, ys
+    Ks = {l[5] for l in launches}
+    io = {"x": {K: torch.randn((batch, K), device=dev).to(torch.bfloat16) for K in Ks},
+          "res": {K: torch.randn((batch, K), device=dev).to(torch.bfloat16) for K in Ks},
+          "h": {K: torch.empty((batch, K), dtype=torch.bfloat16, device=dev) for K in Ks},
+          "xn": {K: torch.empty((batch, K), dtype=torch.bfloat16, device=dev) for K in Ks},
+          "nw": {K: torch.ones(K, dtype=torch.bfloat16, device=dev) for K in Ks},
+          "gu": {K: torch.randn((batch, 2 * K), device=dev).to(torch.bfloat16) for K in Ks},
+          "y": {N: torch.empty((batch, N), dtype=torch.bfloat16, device=dev) for N in {l[6] for l in launches}}}
+    return io
 
 
-def _launch_all(launches, xs, ys, bits):
+def _launch_all(launches, io, bits):
     from shardcompute_amd import _lib
-    for name, wq, s, b, K, N in launches:
-        _lib.qmm(xs[K], wq, s, b, bits=bits, out=ys[N])
+    for name, pro, wq, s, b, K, N in launches:
+        if pro == "norm":
+            _lib.qmm_rmsnorm(io["x"][K], io["nw"][K], 1e-5, wq, s, b, residual=io["res"][K], h_out=io["h"][K],
+                             xn_out=io["xn"][K], bits=bits, out=io["y"][N])
+        else:
+            _lib.qmm(io["x"][K], wq, s, b, bits=bits, out=io["y"][N])
 
 
 def time_gemv_launches(model, batch, bits, reps):
@@ -162,14 +176,14 @@ def time_gemv_launches(model, batch, bits, reps):
     The same is done per projection kind for the per-shape breakdown."""
     import torch
     launches = gemv_launches(model)
-    xs, ys = _gemv_io(launches, batch)
+    io = _gemv_io(launches, batch)
 
     def graph_of(ls):
-        _launch_all(ls, xs, ys, bits)          # warm (kernel attributes set outside capture)
+        _launch_all(ls, io, bits)          # warm (kernel attributes set outside capture)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            _launch_all(ls, xs, ys, bits)
+            _launch_all(ls, io, bits)
         return g
 
     def timed(g, n_launch):
@@ -184,13 +198,14 @@ def time_gemv_launches(model, batch, bits, reps):
         return e0.elapsed_time(e1) * 1e3 / (reps * n_launch)
 
     avg_us = timed(graph_of(launches), len(launches))
-    tot_bytes = sum(qmm_bytes(batch, l[5], l[4], bits) for l in launches)
+    tot_bytes = sum(qmm_bytes(batch, l[6], l[5], bits) for l in launches)
     per = {}
     for kind in ("qkv", "o", "gate_up", "down", "lm_head"):
         ls = [l for l in launches if l[0] == kind]
         us = timed(graph_of(ls), len(ls))
-        nb = qmm_bytes(batch, ls[0][5], ls[0][4], bits)
-        per[kind] = {"K": ls[0][4], "N": ls[0][5], "avg_us": round(us, 3), "GBs": round(nb / (us * 1e-6) / 1e9, 1)}
+        nb = qmm_bytes(batch, ls[0][6], ls[0][5], bits)
+        per[kind] = {"K": ls[0][5], "N": ls[0][6], "prologue": ls[0][1] or "none", "avg_us": round(us, 3),
+                     "GBs": round(nb / (us * 1e-6) / 1e9, 1)}
     bpl = tot_bytes / len(launches)
     log(f"gemv: {len(launches)} launches/step, avg {avg_us:.3f} us, {bpl / 1e6:.2f} MB/launch, "
         f"{bpl / (avg_us * 1e-6) / 1e9:.0f} GB/s")
@@ -202,9 +217,9 @@ def eager_gemv_passes(model, batch, bits, passes):
     """The same launches, eager (for hardware-counter runs, one dispatch at a time)."""
     import torch
     launches = gemv_launches(model)
-    xs, ys = _gemv_io(launches, batch)
+    io = _gemv_io(launches, batch)
     for _ in range(passes):
-        _launch_all(launches, xs, ys, bits)
+        _launch_all(launches, io, bits)
     torch.cuda.synchronize()
     return launches
 
@@ -229,9 +244,9 @@ def cpu_baseline(model, batch, bits, seconds):
     threads = cref.default_threads()
     launches = gemv_launches(model)
     layer0 = launches[:4]
-    name, lwq, ls, lb, K, N = launches[-1]
+    name, _, lwq, ls, lb, K, N = launches[-1]
     rows = N // 32
-    sample = [(u32(l[1]), u16(l[2]), u16(l[3]), l[4]) for l in layer0]
+    sample = [(u32(l[2]), u16(l[3]), u16(l[4]), l[5]) for l in layer0]
     lm = (u32(lwq[:rows]), u16(ls[:rows]), u16(lb[:rows]), K)
     rng = np.random.default_rng(0)
     xs = {k: (rng.standard_normal((batch, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)

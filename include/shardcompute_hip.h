@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 2
+#define SC_ABI_VERSION 3
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -110,6 +110,22 @@ int sc_dequantize_bf16(const uint32_t *wq, const uint16_t *scales, const uint16_
  */
 int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int group_size, uint32_t *wq,
                        uint16_t *scales, uint16_t *biases, void *hip_stream);
+
+/*
+ * y = qmm(xn) with xn = RMSNorm(x + residual) (residual optional): the
+ * normalisation that precedes a projection, applied by the decode GEMV while it
+ * stages its input rows (M <= 8), else by the standalone sc_rms_norm_bf16 first.
+ * On return xn_out [M, K] holds xn and, when a residual is given and h_out_or_null
+ * is not null, h_out [M, K] holds x + residual.  Outputs must not overlap x or the
+ * residual.  Replaces RMSNorm.__call__ (src/shardcompute/parallel/transformer.py:46-61)
+ * followed by the first projection that reads it (attention.py:406-408 after
+ * transformer.py:240, mlp.py:241-242 after transformer.py:249, and the lm_head
+ * after transformer.py:562).
+ */
+int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,
+                        uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
+                        const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N,
+                        int64_t K, int bits, int group_size, void *hip_stream);
 
 /* ------------------------------------------------------------------------------
  * Decoder wiring around the quantized linears.  The cache length (the number of

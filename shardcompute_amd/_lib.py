@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -27,6 +27,7 @@ EXPORTS = (
     "sc_qembed_gather_bf16",
     "sc_dequantize_bf16",
     "sc_quantize_affine",
+    "sc_qmm_rmsnorm_bf16",
     "sc_rms_norm_bf16",
     "sc_rope_append_kv_bf16",
     "sc_attention_workspace_bytes",
@@ -76,6 +77,8 @@ def load():
         lib.sc_quantize_affine.argtypes = [p, i64, i64, i32, i32, p, p, p, p]
         lib.sc_quantize_affine.restype = i32
         f32 = ctypes.c_float
+        lib.sc_qmm_rmsnorm_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
+        lib.sc_qmm_rmsnorm_bf16.restype = i32
         lib.sc_rms_norm_bf16.argtypes = [p, p, p, p, p, i64, i64, f32, p]
         lib.sc_rms_norm_bf16.restype = i32
         lib.sc_rope_append_kv_bf16.argtypes = [p, i64, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, p]
@@ -171,6 +174,58 @@ def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO,
         sink.append((ev0, ev1, M, N, K, bits))
     _check(rc, "sc_qmm_bf16")
     return y.reshape(*lead, N)
+
+
+def _qmm_common(wq, scales, biases, bias, bits, group_size, K):
+    _bf16(scales, "scales"), _bf16(biases, "biases")
+    wq = _u32(wq)
+    N = wq.shape[0]
+    if wq.dim() != 2 or wq.shape[1] * (32 // bits) != K:
+        raise ValueError(f"packed weight {tuple(wq.shape)} does not match K={K} at {bits} bits")
+    G = K // group_size
+    if scales.shape != (N, G) or biases.shape != (N, G):
+        raise ValueError(f"scales/biases must be [{N}, {G}], got {tuple(scales.shape)} / {tuple(biases.shape)}")
+    if bias is not None:
+        _bf16(bias, "bias")
+        if bias.shape != (N,):
+            raise ValueError(f"bias must be [{N}], got {tuple(bias.shape)}")
+        bias = bias.contiguous()
+    return wq.contiguous(), scales.contiguous(), biases.contiguous(), bias, N
+
+
+def _rows(t, K, name):
+    if t.dtype != torch.bfloat16 or t.shape[-1] != K or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous bf16 [..., {K}] tensor")
+    return t
+
+
+def qmm_rmsnorm(x, norm_weight, eps, wq, scales, biases, residual=None, h_out=None, xn_out=None, bias=None,
+                bits=4, group_size=64, out=None):
+    """y = qmm(RMSNorm(x + residual)) with the norm fused into the decode GEMV.
+
+    Returns (y, xn); ``h_out`` (when given with a residual) receives x + residual.
+    Outputs must be distinct from x and the residual."""
+    lib = load()
+    _require_gpu(x, norm_weight, wq, scales, biases, residual, h_out, xn_out, bias, out)
+    K = x.shape[-1]
+    _rows(x, K, "x")
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    wq, scales, biases, bias, N = _qmm_common(wq, scales, biases, bias, bits, group_size, K)
+    if residual is not None:
+        _rows(residual, K, "residual")
+    if h_out is not None:
+        _rows(h_out, K, "h_out")
+    if norm_weight.shape != (K,) or norm_weight.dtype != torch.bfloat16:
+        raise ValueError(f"norm weight must be bf16 [{K}]")
+    xn = xn_out if xn_out is not None else torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    _rows(xn, K, "xn_out")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    rc = lib.sc_qmm_rmsnorm_bf16(_ptr(x), _ptr(residual), _ptr(norm_weight.contiguous()), float(eps), _ptr(h_out),
+                                 _ptr(xn), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y), M, N, K, bits,
+                                 group_size, _stream(x))
+    _check(rc, "sc_qmm_rmsnorm_bf16")
+    return y.reshape(*lead, N), xn.reshape(*lead, K)
 
 
 def vocab_gather(ids, table, vocab_start=0, out=None):

@@ -13,7 +13,9 @@
 namespace sc {
 
 int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
-                        const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+                     const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
+                     const DmaFused *fused = nullptr);
+bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K);
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
                    uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -44,6 +46,8 @@ int launch_argmax(const uint16_t *logits, long rows, long V, int32_t *ids, int32
                   long tok_cols, const int32_t *step, hipStream_t stream);
 int launch_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, long n, hipStream_t stream);
 int launch_add_i32(int32_t *p, long n, int32_t delta, hipStream_t stream);
+
+constexpr int PRO_NORM_KIND = 1;
 
 static thread_local char g_err[512] = "";
 
@@ -157,6 +161,44 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
     }
     if (path == SC_QMM_PATH_GEMM) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
     return set_error(SC_EINVAL, "qmm: unknown path %d", path);
+}
+
+static bool overlap(const void *a, size_t an, const void *b, size_t bn) {
+    if (!a || !b) return false;
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return x < y + bn && y < x + an;
+}
+
+// The quantized product of a normalised input: RMSNorm of x (+ res).  The decode
+// GEMV applies the norm while staging its rows; otherwise the standalone kernel
+// writes x_out and the product reads it.  Either way x_out (and h_out) hold the
+// staged rows afterwards.
+static int qmm_fused(int kind, const uint16_t *x, const uint16_t *res, const uint16_t *nw, float eps,
+                     uint16_t *h_out, uint16_t *x_out, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                     const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits, int group_size,
+                     void *stream) {
+    const char *what = "qmm_rmsnorm";
+    int rc = check_qmm(x_out, wq, s, b, y, M, N, K, bits, group_size);
+    if (rc) return rc;
+    if (!x || !nw) return set_error(SC_EINVAL, "%s: null pointer argument", what);
+    if (K % 8) return set_error(SC_EINVAL, "%s: K=%lld must be a multiple of 8", what, (long long)K);
+    if (!aligned(x, 16) || !aligned(res, 16) || !aligned(nw, 16) || !aligned(h_out, 16))
+        return set_error(SC_EINVAL, "%s: activation pointers must be 16-byte aligned", what);
+    const size_t row_bytes = (size_t)M * K * 2, in_bytes = row_bytes;
+    if (overlap(x_out, row_bytes, x, in_bytes) || overlap(x_out, row_bytes, res, row_bytes) ||
+        overlap(h_out, row_bytes, x, in_bytes) || overlap(h_out, row_bytes, res, row_bytes) ||
+        overlap(h_out, row_bytes, x_out, row_bytes))
+        return set_error(SC_EINVAL, "%s: outputs must not overlap the inputs (other workgroups still read them)",
+                         what);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (qgemv_dma_eligible(x_out, wq, s, b, (int)M, (int)K)) {
+        DmaFused f{kind, res, nw, eps, h_out, x_out};
+        rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, &f);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
+    rc = launch_rms_norm(x, res, nw, x_out, h_out, M, K, eps, st);
+    if (rc) return rc;
+    return qmm_dispatch(x_out, wq, s, b, bias, y, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
 }
 
 }  // namespace sc
@@ -274,5 +316,14 @@ int sc_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n, 
 int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream) {
     return launch_add_i32(counters, n, delta, reinterpret_cast<hipStream_t>(hip_stream));
 }
+
+int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,
+                        uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
+                        const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N,
+                        int64_t K, int bits, int group_size, void *hip_stream) {
+    return qmm_fused(PRO_NORM_KIND, x, residual_or_null, norm_weight, eps, residual_or_null ? h_out_or_null : nullptr,
+                     xn_out, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream);
+}
+
 
 }  // extern "C"

@@ -19,29 +19,6 @@ namespace {
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-
-// x*y and x+y rounded once each, never fused into an FMA (the IR carries no
-// contract flag; HIP's __fmul_rn is a plain product that contracts after inlining)
-__device__ __forceinline__ float mul_rn(float x, float y) {
-#pragma clang fp contract(off)
-    return x * y;
-}
-__device__ __forceinline__ float add_rn(float x, float y) {
-#pragma clang fp contract(off)
-    return x + y;
-}
-
-// fp32 value of element e (0..7) of 8 packed bf16
-__device__ __forceinline__ float bfe(uint4 v, int e) {
-    const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
-    return (e & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
-}
-
 }  // namespace
 
 // ---------------------------------------------------------------- RMSNorm
@@ -52,7 +29,6 @@ __device__ __forceinline__ float bfe(uint4 v, int e) {
 // per-element arithmetic is IEEE single ops in the reference's order (divide by
 // the root, then multiply by the weight); contraction to FMA is switched off in
 // every kernel whose output is compared bit for bit.
-constexpr int NORM_THREADS = 256;
 constexpr int NORM_MAXV = 8;   // D <= 256 * 8 * 8 = 16384
 
 __global__ void __launch_bounds__(NORM_THREADS)
@@ -71,25 +47,11 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
         if (idx < nv) {
             uint4 v = xr[idx];
             if (rr) {
-                const uint4 r = rr[idx];
-                uint32_t o[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t a = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
-                    const uint32_t b = e == 0 ? r.x : e == 1 ? r.y : e == 2 ? r.z : r.w;
-                    const float lo = add_rn(__uint_as_float(a << 16), __uint_as_float(b << 16));
-                    const float hi = add_rn(__uint_as_float(a & 0xFFFF0000u), __uint_as_float(b & 0xFFFF0000u));
-                    o[e] = pack_bf16x2(lo, hi);
-                }
-                v = make_uint4(o[0], o[1], o[2], o[3]);
+                v = add_bf16x8(v, rr[idx]);
                 if (h_out) reinterpret_cast<uint4 *>(h_out + (size_t)row * D)[idx] = v;
             }
             hv[i] = v;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float f = bfe(v, e);
-                ss = add_rn(ss, mul_rn(f, f));
-            }
+            ss = sumsq_bf16x8(ss, v);
         }
     }
     __shared__ float red[NORM_THREADS / 64];
@@ -99,23 +61,13 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
     float tot = 0.f;
 #pragma unroll
     for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
-    const float root = __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)D), eps));
+    const float root = rms_root(tot, D, eps);
     const uint4 *wr = reinterpret_cast<const uint4 *>(w);
     uint4 *yr = reinterpret_cast<uint4 *>(y + (size_t)row * D);
 #pragma unroll
     for (int i = 0; i < NORM_MAXV; ++i) {
         const int idx = threadIdx.x + i * NORM_THREADS;
-        if (idx < nv) {
-            const uint4 wv = wr[idx];
-            uint32_t o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float lo = mul_rn(__fdiv_rn(bfe(hv[i], 2 * e), root), bfe(wv, 2 * e));
-                const float hi = mul_rn(__fdiv_rn(bfe(hv[i], 2 * e + 1), root), bfe(wv, 2 * e + 1));
-                o[e] = pack_bf16x2(lo, hi);
-            }
-            yr[idx] = make_uint4(o[0], o[1], o[2], o[3]);
-        }
+        if (idx < nv) yr[idx] = norm_bf16x8(hv[i], wr[idx], root);
     }
 }
 
@@ -448,7 +400,6 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 // (parallel/mlp.py:161-162, 241-245).
 __global__ void __launch_bounds__(256)
 silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, long rows, int I) {
-#pragma clang fp contract(off)
     const long nv = rows * (I >> 3);
     const int vpr = I >> 3;
     for (long idx = (long)blockIdx.x * blockDim.x + threadIdx.x; idx < nv; idx += (long)gridDim.x * blockDim.x) {
@@ -456,19 +407,7 @@ silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, lon
         const int v = (int)(idx - r * vpr);
         const uint4 gv = reinterpret_cast<const uint4 *>(gu + (size_t)r * 2 * I)[v];
         const uint4 uv = reinterpret_cast<const uint4 *>(gu + (size_t)r * 2 * I + I)[v];
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float res[2];
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const float gg = bfe(gv, 2 * e + k);
-                const float sig = __fdiv_rn(gg, add_rn(1.f, expf(-gg)));
-                res[k] = mul_rn(sig, bfe(uv, 2 * e + k));
-            }
-            o[e] = pack_bf16x2(res[0], res[1]);
-        }
-        reinterpret_cast<uint4 *>(out + (size_t)r * I)[v] = make_uint4(o[0], o[1], o[2], o[3]);
+        reinterpret_cast<uint4 *>(out + (size_t)r * I)[v] = silu_mul_bf16x8(gv, uv);
     }
 }
 
@@ -534,16 +473,8 @@ argmax_kernel(const uint16_t *__restrict__ logits, long V, int32_t *__restrict__
 // no normalisation follows).
 __global__ void __launch_bounds__(256)
 add_bf16_kernel(const uint16_t *__restrict__ a, const uint16_t *__restrict__ b, uint16_t *__restrict__ out, long nv) {
-#pragma clang fp contract(off)
-    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (long)gridDim.x * blockDim.x) {
-        const uint4 x = reinterpret_cast<const uint4 *>(a)[i];
-        const uint4 y = reinterpret_cast<const uint4 *>(b)[i];
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            o[e] = pack_bf16x2(add_rn(bfe(x, 2 * e), bfe(y, 2 * e)), add_rn(bfe(x, 2 * e + 1), bfe(y, 2 * e + 1)));
-        reinterpret_cast<uint4 *>(out)[i] = make_uint4(o[0], o[1], o[2], o[3]);
-    }
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (long)gridDim.x * blockDim.x)
+        reinterpret_cast<uint4 *>(out)[i] = add_bf16x8(reinterpret_cast<const uint4 *>(a)[i], reinterpret_cast<const uint4 *>(b)[i]);
 }
 
 __global__ void add_i32_kernel(int32_t *p, int n, int32_t delta) {

@@ -22,11 +22,19 @@
 //   the mantissa of 128.0; W8: q) as operand B of v_mfma_f32_16x16x32_bf16,
 //   x is operand A, W4 spans use A-rows as selectors of the two quantization
 //   groups, and acc += s * P + (b - off * s) * xsum[m, g].
-// * Complete tiles are written from registers; tiles split between waves are
-//   summed with ds_add_f32 and written by the wave that completes them.
+// * Complete tiles are written from registers; a tile split between waves is
+//   summed in wave order from per-wave LDS slots after a barrier, by the wave that
+//   holds its last item (no atomics: results are reproducible run to run).
 #include "sc_common.h"
 
 namespace sc {
+
+// What the kernel does to its input rows while staging them in LDS.
+enum DmaPrologue {
+    PRO_NONE = 0,   // x [M, K] as given
+    PRO_NORM = 1,   // RMSNorm of x (+ res): the input layernorm before q|k|v, the
+                    // post-attention layernorm before gate|up, the final norm before the lm_head
+};
 
 struct DmaArgs {
     const uint16_t *x;
@@ -37,6 +45,13 @@ struct DmaArgs {
     uint16_t *y;
     int M, N, K, G;
     int max_tiles_per_block;
+    int pro;
+    const uint16_t *res;    // PRO_NORM: residual added first (may be null)
+    const uint16_t *nw;     // PRO_NORM: norm weight [K]
+    float eps;
+    uint16_t *h_out;        // PRO_NORM with res: x + res, written by workgroup 0
+    uint16_t *x_out;        // the staged input rows (normalised / gated), written by workgroup 0
+    int dma_stage;          // input rows are staged by LDS-DMA (they fit the staging areas)
 };
 
 namespace {
@@ -46,6 +61,8 @@ constexpr int DMA_PER_ITEM = 5;             // 4 weight + 1 scale/bias instructi
 constexpr int SLOT_W = 4096;                // weight bytes per item
 constexpr int SLOT_BYTES = SLOT_W + 1024;   // + scales (lanes 0-15) and biases (16-31)
 constexpr int DMA_MAX_WAVES = 8;
+constexpr int XMAX = 8;                     // input chunks (16 B) per thread in the staging transform
+constexpr int S2_UNITS = SLOT_W / 1024 + 1; // 1 KB staging units in one ring slot
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
 
@@ -87,6 +104,12 @@ __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask_sgpr, uint3
     return (x & mask_sgpr) | magic_vgpr;
 }
 
+__device__ __forceinline__ void wait_lgkm0() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Wait until at most n vector-memory operations of this wave are outstanding
 // (lgkmcnt / expcnt untouched).
 template <int n>
@@ -97,17 +120,12 @@ __device__ __forceinline__ void wait_vm() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ void wait_lgkm0() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 }  // namespace
 
 // MR: 1 for a single row of x (only D register 0 of lane-groups 0 and 2 matters),
 // 8 for up to 8 rows.
-template <int BITS, int MR>
+template <int BITS, int MR, int PRO>
 __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a) {
     constexpr int NR = MR == 1 ? 1 : 4;                // D registers that can hold a row < M
     constexpr int SPAN_K = BITS == 4 ? 128 : 64;       // one 64-byte span of a row
@@ -128,27 +146,33 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
 
     const int T = (N + 15) >> 4;
     const int P = gridDim.x;
-    const int t_begin = (int)(((long)blockIdx.x * T) / P);
-    const int t_end = (int)(((long)(blockIdx.x + 1) * T) / P);
+    const int t_begin = (int)(blockIdx.x * (unsigned)T / (unsigned)P);       // T * P < 2^31 (host)
+    const int t_end = (int)((blockIdx.x + 1) * (unsigned)T / (unsigned)P);
     const int ntl = t_end - t_begin;
     const int CPT = K / ITEM_K;
     const int items = ntl * CPT;
     const int W = K / 8;
     const int xstride = W + 1;
 
-    // LDS carve-up: rings | x (M rows + zero row) | xsum | tile accumulators | counters | bias
+    // LDS carve-up: rings | x (M rows + zero row) | xsum | split-tile partials | bias
     uint8_t *ring = smem + (size_t)wave * RING * SLOT_BYTES;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
     uint4 *xl = reinterpret_cast<uint4 *>(smem + (size_t)nwaves * RING * SLOT_BYTES);
     float *xs = reinterpret_cast<float *>(xl + (size_t)(M + 1) * xstride);
-    float *accl = xs + M * G;
-    int *cnt = reinterpret_cast<int *>(accl + a.max_tiles_per_block * M * 16);
+    // a wave's range splits at most two tiles (its first and its last): one partial
+    // slot each; the last contributor to arrive sums the slots in wave order, so
+    // results are reproducible without a barrier
+    float *part_l = xs + M * G;
     // the bias slice lives in LDS: a global load inside the ring loop would make the
     // compiler wait for every outstanding DMA
-    uint16_t *bias_l = reinterpret_cast<uint16_t *>(cnt + a.max_tiles_per_block);
+    uint16_t *bias_l = reinterpret_cast<uint16_t *>(part_l + (size_t)nwaves * 2 * M * 16);
+    int *cnt = reinterpret_cast<int *>(bias_l + ((a.max_tiles_per_block * 16 + 1) & ~1));   // items summed per tile
 
-    const int lo = (int)(((long)wave * items) / nwaves);
-    const int hi = (int)(((long)(wave + 1) * items) / nwaves);
+    // waves split the items evenly; 4 or 8 waves, so the division is a shift (a
+    // 64-bit or variable division costs a software routine on every use)
+    const int nwl2 = 31 - __clz(nwaves);
+    const int lo = (wave * items) >> nwl2;
+    const int hi = ((wave + 1) * items) >> nwl2;
 
     // ---- item DMA: 4 x (4 rows x 256 B, row-rotated) + scales/biases of the 16 rows.
     // Pointers advance incrementally; they are rebuilt only when the tile changes.
@@ -183,24 +207,167 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
         }
     };
 
+    // ---- input rows.  Every workgroup stages the same rows with the same arithmetic,
+    // so a fused normalisation or gate yields identical inputs in all of them (and
+    // the same bits as the standalone kernels, which share the math and the row
+    // partition: 256 threads per row, thread t holding chunks t, t + 256, ...).
+    // When they fit, the raw rows arrive by LDS-DMA issued before the weight ring
+    // starts: x (or gate|up) into the x area, residual and norm weight into the
+    // third ring slot of every wave (idle until the ring loop), and only they are
+    // waited for.  Otherwise (and for linears with a bias) ordinary loads stage
+    // them, which the compiler waits for together with the weight DMA.
     const bool has_work = hi > lo;
+    const bool dstage = PRO == PRO_NONE && a.dma_stage != 0;   // (the norm prologue stages with ordinary loads)
+    const int groups = blockDim.x / NORM_THREADS;
+    const int gsel = tid / NORM_THREADS, tg = tid - gsel * NORM_THREADS;
+    const int WPT = (W + NORM_THREADS - 1) / NORM_THREADS;    // norm chunks per row and thread
+    const uint32_t xraw = (uint32_t)(uintptr_t)xl;
+    auto s2_unit = [&](int u) -> uint32_t {
+        return (uint32_t)(uintptr_t)(smem + (size_t)(u / S2_UNITS) * RING * SLOT_BYTES + 2 * SLOT_BYTES +
+                                     (size_t)(u % S2_UNITS) * 1024);
+    };
+    const int ru = (int)(((size_t)M * K * 2 + 1023) / 1024);   // staging units of the residual rows
+    if (dstage) {
+        auto stage = [&](const uint16_t *src, size_t bytes, int unit0, bool to_s2) {
+            const int units = (int)((bytes + 1023) / 1024);
+            for (int u = wave; u < units; u += nwaves) {
+                const size_t off = (size_t)u * 1024 + 16 * lane;
+                const uint32_t dst = to_s2 ? s2_unit(unit0 + u) : xraw + (uint32_t)u * 1024;
+                if (off < bytes) dma16(reinterpret_cast<const uint8_t *>(src) + off, dst);
+            }
+        };
+        stage(a.x, (size_t)M * K * 2, 0, false);
+        if (PRO == PRO_NORM) {
+            if (a.res) stage(a.res, (size_t)M * K * 2, 0, true);
+            stage(a.nw, (size_t)K * 2, ru, true);
+        }
+    }
     if (has_work) {
 #pragma unroll
         for (int k = 0; k < RING - 1; ++k) issue(k);
     }
-
-    // ---- x, zero row, per-group sums, accumulators (ordinary loads, done before the ring loop)
-    for (int idx = tid; idx < M * W; idx += blockDim.x) {
-        const int m = idx / W, w = idx - (idx / W) * W;
-        const uint4 v = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * K + (size_t)w * 8);
-        xl[m * xstride + w] = BITS == 4 ? perm_w4x(v) : v;
+    if (dstage) {
+        if (has_work) wait_vm<DMA_PER_ITEM * (RING - 1)>();
+        else wait_vm<0>();
+        __syncthreads();
+        const uint4 *raw = reinterpret_cast<const uint4 *>(xl);
+        auto s2_chunk = [&](size_t chunk) -> uint4 {      // 16-byte chunk of the ring-slot staging area
+            const size_t bo = chunk * 16;
+            return *reinterpret_cast<const uint4 *>(reinterpret_cast<const uint8_t *>(smem) +
+                                                    (s2_unit((int)(bo / 1024)) - (uint32_t)(uintptr_t)smem) +
+                                                    bo % 1024);
+        };
+        uint4 v[XMAX];
+        if (PRO == PRO_NORM) {
+            __shared__ float red[8][NORM_THREADS / 64];
+            __shared__ float root_l[8];
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < XMAX; ++i) {
+                const int ri = i / WPT, m = gsel + groups * ri, w = tg + NORM_THREADS * (i - ri * WPT);
+                const bool ok = m < M && w < W && ri * groups < M;
+                if (ok) {
+                    v[i] = raw[m * W + w];
+                    if (a.res) {
+                        v[i] = add_bf16x8(v[i], s2_chunk((size_t)m * W + w));
+                        if (blockIdx.x == 0 && a.h_out)
+                            *reinterpret_cast<uint4 *>(a.h_out + (size_t)m * K + (size_t)w * 8) = v[i];
+                    }
+                    ss = sumsq_bf16x8(ss, v[i]);
+                }
+                if ((i % WPT) == WPT - 1 || i == XMAX - 1) {      // end of this thread's chunks of a row
+                    const float tot = wave_sum(ss);
+                    if (m < M && (tg & 63) == 0) red[m][tg >> 6] = tot;
+                    ss = 0.f;
+                }
+            }
+            __syncthreads();                                        // raw x fully read: the area is reused below
+            if (tid < M) {
+                float tot = 0.f;
+#pragma unroll
+                for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[tid][i];
+                root_l[tid] = rms_root(tot, K, a.eps);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < XMAX; ++i) {
+                const int ri = i / WPT, m = gsel + groups * ri, w = tg + NORM_THREADS * (i - ri * WPT);
+                if (m < M && w < W && ri * groups < M) {
+                    const uint4 o = norm_bf16x8(v[i], s2_chunk((size_t)ru * 64 + w), root_l[m]);
+                    if (blockIdx.x == 0 && a.x_out) *reinterpret_cast<uint4 *>(a.x_out + (size_t)m * K + (size_t)w * 8) = o;
+                    xl[m * xstride + w] = BITS == 4 ? perm_w4x(o) : o;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < XMAX; ++i) {
+                const int idx = tid + i * (int)blockDim.x;
+                if (idx < M * W) {
+                    const int m = idx / W, w = idx - (idx / W) * W;
+                    v[i] = raw[idx];
+                }
+            }
+            __syncthreads();                                        // raw rows fully read
+#pragma unroll
+            for (int i = 0; i < XMAX; ++i) {
+                const int idx = tid + i * (int)blockDim.x;
+                if (idx < M * W) {
+                    const int m = idx / W, w = idx - (idx / W) * W;
+                    xl[m * xstride + w] = BITS == 4 ? perm_w4x(v[i]) : v[i];
+                }
+            }
+        }
+    } else if (PRO == PRO_NONE) {
+        for (int idx = tid; idx < M * W; idx += blockDim.x) {
+            const int m = idx / W, w = idx - (idx / W) * W;
+            const uint4 v = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * K + (size_t)w * 8);
+            xl[m * xstride + w] = BITS == 4 ? perm_w4x(v) : v;
+        }
+    } else {
+        __shared__ float red[8][NORM_THREADS / 64];
+        __shared__ float root_l[8];
+        for (int idx = tid; idx < M * W; idx += blockDim.x) {
+            const int m = idx / W, w = idx - (idx / W) * W;
+            uint4 v = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * K + (size_t)w * 8);
+            if (a.res) {
+                v = add_bf16x8(v, *reinterpret_cast<const uint4 *>(a.res + (size_t)m * K + (size_t)w * 8));
+                if (blockIdx.x == 0 && a.h_out) *reinterpret_cast<uint4 *>(a.h_out + (size_t)m * K + (size_t)w * 8) = v;
+            }
+            xl[m * xstride + w] = v;
+        }
+        __syncthreads();
+        // per-row sums of squares, 256 threads per row as in the standalone RMSNorm
+        const int groups = blockDim.x / NORM_THREADS;
+        const int gsel = tid / NORM_THREADS, t = tid - gsel * NORM_THREADS;
+        for (int m0 = 0; m0 < M; m0 += groups) {
+            const int m = m0 + gsel;
+            if (m < M) {
+                float ss = 0.f;
+                for (int idx = t; idx < W; idx += NORM_THREADS) ss = sumsq_bf16x8(ss, xl[m * xstride + idx]);
+                ss = wave_sum(ss);
+                if ((t & 63) == 0) red[m][t >> 6] = ss;
+            }
+        }
+        __syncthreads();
+        if (tid < M) {
+            float tot = 0.f;
+#pragma unroll
+            for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[tid][i];
+            root_l[tid] = rms_root(tot, K, a.eps);
+        }
+        __syncthreads();
+        for (int idx = tid; idx < M * W; idx += blockDim.x) {
+            const int m = idx / W, w = idx - (idx / W) * W;
+            const uint4 v = norm_bf16x8(xl[m * xstride + w], reinterpret_cast<const uint4 *>(a.nw)[w], root_l[m]);
+            if (blockIdx.x == 0 && a.x_out) *reinterpret_cast<uint4 *>(a.x_out + (size_t)m * K + (size_t)w * 8) = v;
+            xl[m * xstride + w] = BITS == 4 ? perm_w4x(v) : v;
+        }
     }
-    for (int idx = tid; idx < W; idx += blockDim.x) xl[M * xstride + idx] = make_uint4(0u, 0u, 0u, 0u);
-    for (int idx = tid; idx < ntl * M * 16; idx += blockDim.x) accl[idx] = 0.f;
-    for (int idx = tid; idx < ntl; idx += blockDim.x) cnt[idx] = 0;
     if (a.bias)
         for (int idx = tid; idx < ntl * 16; idx += blockDim.x)
             bias_l[idx] = a.bias[min(t_begin * 16 + idx, N - 1)];
+    for (int idx = tid; idx < W; idx += blockDim.x) xl[M * xstride + idx] = make_uint4(0u, 0u, 0u, 0u);
+    for (int idx = tid; idx < ntl; idx += blockDim.x) cnt[idx] = 0;
     __syncthreads();
     for (int idx = tid; idx < M * G; idx += blockDim.x) {
         const int m = idx / G, g = idx - (idx / G) * G;
@@ -214,10 +381,6 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
         xs[m * G + g] = sum;
     }
     __syncthreads();
-    if (!has_work) {
-        wait_vm<0>();
-        return;
-    }
 
     // A operand rows (zero row for lanes that carry no x) and D-row mapping
     const int am = (BITS == 4) ? (j & 7) : j;
@@ -242,6 +405,7 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
             a.y[(size_t)m * N + nn] = (uint16_t)o;
         }
     };
+    int fin_a = -1, fin_b = -1;      // split tiles this wave completes
     auto flush = [&]() {
         f4 fin = acc;
         if (BITS == 4) {
@@ -254,19 +418,20 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
                 for (int r = 0; r < 4; ++r) write_out(cur_tile, em0 + r, j, fin[r]);
             }
         } else {
-            float *slot = accl + cur_tile * M * 16;
             if (q < 2) {
+                float *pl = part_l + ((size_t)wave * 2 + (cur_tile == lo / CPT ? 0 : 1)) * M * 16;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (em0 + r < M) atomicAdd(&slot[(em0 + r) * 16 + j], fin[r]);
+                    if (em0 + r < M) pl[(em0 + r) * 16 + j] = fin[r];
             }
-            wait_lgkm0();
+            wait_lgkm0();                                       // slot written before the count
             int done = 0;
             if (lane == 0) done = (atomicAdd(&cnt[cur_tile], chunks_in_acc) + chunks_in_acc) == CPT;
             done = __shfl(done, 0);
+            // the last contributor sums the tile after its ring loop (keeps the loop short)
             if (done) {
-                wait_lgkm0();
-                for (int o = lane; o < M * 16; o += 64) write_out(cur_tile, o >> 4, o & 15, slot[o]);
+                if (fin_a < 0) fin_a = cur_tile;
+                else fin_b = cur_tile;
             }
         }
         acc = f4{0.f, 0.f, 0.f, 0.f};
@@ -341,29 +506,54 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
     };
 
     // ---- ring: item lo+i sits in slot i % RING; RING-1 items are always in flight
-    const int n_my = hi - lo;
-    int i = 0;
-    for (; i + RING <= n_my; i += RING) {
+    if (has_work) {
+        const int n_my = hi - lo;
+        int i = 0;
+        for (; i + RING <= n_my; i += RING) {
 #pragma unroll
-        for (int k = 0; k < RING; ++k) {
+            for (int k = 0; k < RING; ++k) {
+                issue((k + RING - 1) % RING);
+                wait_vm<DMA_PER_ITEM * (RING - 1)>();
+                compute(lo + i + k, k);
+            }
+        }
+        for (int k = 0; i < n_my; ++i, ++k) {
             issue((k + RING - 1) % RING);
             wait_vm<DMA_PER_ITEM * (RING - 1)>();
-            compute(lo + i + k, k);
+            compute(lo + i, k % RING);
+        }
+        flush();
+    }
+    wait_vm<0>();
+    // ---- split tiles whose last contributor this wave was: sum the partial slots in
+    // wave order (every contributor wrote its slot before counting itself)
+    for (int f = 0; f < 2; ++f) {
+        const int tile = f == 0 ? fin_a : fin_b;
+        if (tile < 0) continue;
+        wait_lgkm0();
+        const int ts = tile * CPT, te = ts + CPT;
+        for (int o = lane; o < M * 16; o += 64) {
+            float v = 0.f;
+            for (int w2 = 0; w2 < nwaves; ++w2) {
+                const int lo2 = (w2 * items) >> nwl2, hi2 = ((w2 + 1) * items) >> nwl2;
+                if (hi2 <= lo2 || hi2 <= ts || lo2 >= te) continue;
+                v += part_l[((size_t)w2 * 2 + (lo2 / CPT == tile ? 0 : 1)) * M * 16 + o];
+            }
+            write_out(tile, o >> 4, o & 15, v);
         }
     }
-    for (int k = 0; i < n_my; ++i, ++k) {
-        issue((k + RING - 1) % RING);
-        wait_vm<DMA_PER_ITEM * (RING - 1)>();
-        compute(lo + i, k % RING);
-    }
-    flush();
-    wait_vm<0>();
 }
 
 // ---------------------------------------------------------------- host side
 
+bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K) {
+    (void)x;
+    return M >= 1 && M <= 8 && K % 512 == 0 && !((uintptr_t)s % 16) && !((uintptr_t)b % 16) && !((uintptr_t)wq % 16);
+}
+
 int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
-                     const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream) {
+                     const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
+                     const DmaFused *fused) {
     if (M < 1 || M > 8) return SC_EUNSUPPORTED;
     if (K % 512) return SC_EUNSUPPORTED;                       // 16-byte aligned scale rows, whole items
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16) || ((uintptr_t)wq % 16)) return SC_EUNSUPPORTED;
@@ -381,14 +571,37 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
         while (P > 1 && (long)T * CPT < (long)P * w) P /= 2;
         const int tpb = (T + P - 1) / P;
         lds = (size_t)w * RING * SLOT_BYTES + (size_t)(M + 1) * (K / 8 + 1) * 16 + (size_t)M * G * 4 +
-              (size_t)tpb * M * 16 * 4 + (size_t)tpb * 4 + (size_t)tpb * 16 * 2;
-        if (lds <= (size_t)lds_cap) { waves = w; break; }
+              (size_t)w * 2 * M * 16 * 4 + (size_t)tpb * 16 * 2 + 4 + (size_t)tpb * 4;
+        if (lds + 256 <= (size_t)lds_cap) { waves = w; break; }   // + the norm prologue's static LDS
     }
     if (!waves) return SC_EUNSUPPORTED;
     const int max_tpb = (T + P - 1) / P;
+    // the kernel's tile and item ranges use 32-bit products
+    if ((long)T * P >= (1L << 31) || (long)max_tpb * CPT * DMA_MAX_WAVES >= (1L << 31)) return SC_EUNSUPPORTED;
     DmaArgs a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
     a.M = M; a.N = N; a.K = K; a.G = G; a.max_tiles_per_block = max_tpb;
+    a.pro = PRO_NONE; a.res = nullptr; a.nw = nullptr; a.eps = 0.f; a.h_out = nullptr; a.x_out = nullptr;
+    if (fused) {
+        a.pro = fused->kind; a.res = fused->res; a.nw = fused->norm_weight; a.eps = fused->eps;
+        a.h_out = fused->h_out; a.x_out = fused->x_out;
+    }
+    {
+        // LDS-DMA staging needs 16-byte rows, the raw rows within the x area, the
+        // residual and norm weight within the waves' third ring slots, and at most
+        // XMAX chunks per thread in the transform
+        const int threads = 64 * waves, W = K / 8;
+        const int groups = threads / NORM_THREADS;
+        const size_t x_area = (size_t)(M + 1) * (W + 1) * 16;
+        const size_t s2_area = (size_t)waves * S2_UNITS * 1024;
+        // (measured: the norm prologue is faster with ordinary loads)
+        bool ok = !bias && !((uintptr_t)x % 16) && a.pro == PRO_NONE;
+        const int chunks = (M * W + threads - 1) / threads;
+        ok = ok && chunks <= XMAX && (size_t)M * K * 2 <= x_area;
+        (void)groups;
+        (void)s2_area;
+        a.dma_stage = ok;
+    }
     auto launch = [&](auto kern, int &configured) -> int {
         if (lds > 65536 && (int)lds > configured) {
             SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -399,10 +612,24 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
         SC_HIP_CHECK(hipGetLastError());
         return SC_OK;
     };
-    static int cfg4 = 0, cfg8 = 0;
-    static int cfg41 = 0, cfg81 = 0;
-    if (M == 1) return bits == 4 ? launch(qgemv_dma_kernel<4, 1>, cfg41) : launch(qgemv_dma_kernel<8, 1>, cfg81);
-    return bits == 4 ? launch(qgemv_dma_kernel<4, 8>, cfg4) : launch(qgemv_dma_kernel<8, 8>, cfg8);
+    // one instantiation per prologue keeps each kernel's code short (these launches
+    // are latency-bound, and a cold instruction fetch of unused prologue code shows)
+    static int cfg[2][2][2] = {};
+    const int bi = bits == 4 ? 0 : 1, mi = M == 1 ? 0 : 1, pi = a.pro;
+    if (bits == 4) {
+        if (M == 1) {
+            if (pi == PRO_NORM) return launch(qgemv_dma_kernel<4, 1, PRO_NORM>, cfg[bi][mi][pi]);
+            return launch(qgemv_dma_kernel<4, 1, PRO_NONE>, cfg[bi][mi][pi]);
+        }
+        if (pi == PRO_NORM) return launch(qgemv_dma_kernel<4, 8, PRO_NORM>, cfg[bi][mi][pi]);
+        return launch(qgemv_dma_kernel<4, 8, PRO_NONE>, cfg[bi][mi][pi]);
+    }
+    if (M == 1) {
+        if (pi == PRO_NORM) return launch(qgemv_dma_kernel<8, 1, PRO_NORM>, cfg[bi][mi][pi]);
+        return launch(qgemv_dma_kernel<8, 1, PRO_NONE>, cfg[bi][mi][pi]);
+    }
+    if (pi == PRO_NORM) return launch(qgemv_dma_kernel<8, 8, PRO_NORM>, cfg[bi][mi][pi]);
+    return launch(qgemv_dma_kernel<8, 8, PRO_NONE>, cfg[bi][mi][pi]);
 }
 
 }  // namespace sc

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <math.h>
 
 namespace sc {
 
@@ -25,6 +26,90 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return f2bf(lo) | (f2bf(hi) << 16);
 }
+
+// ---------------------------------------------------------------- exact elementwise math
+//
+// The kernels whose outputs are compared bit for bit (RMSNorm, residual add, SiLU
+// gate, RoPE) compute with these: x*y and x+y rounded once each and never fused
+// into an FMA (the IR carries no contract flag; HIP's __fmul_rn is a plain
+// product that contracts after inlining).  The standalone kernels and the GEMV
+// prologues that fuse the same ops share them, so both give identical bits.
+
+__device__ __forceinline__ float mul_rn(float x, float y) {
+#pragma clang fp contract(off)
+    return x * y;
+}
+__device__ __forceinline__ float add_rn(float x, float y) {
+#pragma clang fp contract(off)
+    return x + y;
+}
+
+// fp32 value of element e (0..7) of 8 packed bf16
+__device__ __forceinline__ float bfe(uint4 v, int e) {
+    const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
+    return (e & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
+}
+
+// xor-tree sum over the 64 lanes (every lane gets the same total)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+// bf16(a + b), 8 packed bf16
+__device__ __forceinline__ uint4 add_bf16x8(uint4 a, uint4 b) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(add_rn(bfe(a, 2 * e), bfe(b, 2 * e)), add_rn(bfe(a, 2 * e + 1), bfe(b, 2 * e + 1)));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// ss + h_0^2 + ... + h_7^2, left to right
+__device__ __forceinline__ float sumsq_bf16x8(float ss, uint4 v) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float f = bfe(v, e);
+        ss = add_rn(ss, mul_rn(f, f));
+    }
+    return ss;
+}
+
+// sqrt(mean + eps) from the row's sum of squares (transformer.py:52)
+__device__ __forceinline__ float rms_root(float tot, int D, float eps) {
+    return __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)D), eps));
+}
+
+// bf16((h / root) * w): divide by the root, then scale (transformer.py:55)
+__device__ __forceinline__ uint4 norm_bf16x8(uint4 h, uint4 w, float root) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        o[e] = pack_bf16x2(mul_rn(__fdiv_rn(bfe(h, 2 * e), root), bfe(w, 2 * e)),
+                           mul_rn(__fdiv_rn(bfe(h, 2 * e + 1), root), bfe(w, 2 * e + 1)));
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// bf16((g / (1 + exp(-g))) * u) (parallel/mlp.py:161-162, 244)
+__device__ __forceinline__ uint4 silu_mul_bf16x8(uint4 g, uint4 u) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float r[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float gg = bfe(g, 2 * e + k);
+            r[k] = mul_rn(__fdiv_rn(gg, add_rn(1.f, expf(-gg))), bfe(u, 2 * e + k));
+        }
+        o[e] = pack_bf16x2(r[0], r[1]);
+    }
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Row RMS partition shared by every kernel that normalises a row: 256 threads,
+// thread t sums chunks t, t + 256, ... (8 elements each, in order), then each
+// wave reduces with wave_sum and the 4 wave partials are added in order.
+constexpr int NORM_THREADS = 256;
 
 // ---------------------------------------------------------------- MLX affine codes
 //
@@ -88,6 +173,17 @@ struct SplitKScratch {
     unsigned *counters = nullptr;
 };
 int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out);
+
+// Input transformation a decode GEMV can apply while staging its rows (see
+// qgemv_dma.hip): 1 = RMSNorm of x (+ res), 2 = silu(gate) * up of x = gate|up.
+struct DmaFused {
+    int kind;
+    const uint16_t *res;
+    const uint16_t *norm_weight;
+    float eps;
+    uint16_t *h_out;
+    uint16_t *x_out;
+};
 
 }  // namespace sc
 

@@ -94,5 +94,18 @@ class FusedColumns:
             return out
         return y
 
+    def norm_call(self, h, norm, residual=None, h_out=None, xn_out=None, out=None):
+        """The stacked product of ``norm(h + residual)``: the RMSNorm (and residual
+        add, written to ``h_out``) runs inside the quantized kernel.  Returns (y, xn)."""
+        if not self._current():
+            self.build()
+        norm._check()
+        if self.quantized:
+            return _lib.qmm_rmsnorm(h, norm.weight, norm.eps, self._wq, self._s, self._b, residual=residual,
+                                    h_out=h_out, xn_out=xn_out, bias=self._bias, bits=self.bits,
+                                    group_size=self.group_size, out=out)
+        xn = _lib.rms_norm(h, norm.weight, norm.eps, residual=residual, h_out=h_out, out=xn_out)
+        return self(xn, out=out), xn
+
     def split(self, y):
         return torch.split(y, self.widths, dim=-1)

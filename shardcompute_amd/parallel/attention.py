@@ -161,9 +161,13 @@ class ParallelAttention:
     def attend(self, x2, B, S, kv: LayerKV, out=None, qkv_out=None, workspace=None, pos_offset=0):
         """Core of the forward: x2 ``[B*S, hidden]`` -> attention output ``[B*S, local_hidden]``
         (before o_proj), appending the S new positions at ``kv.counters[0]``."""
+        return self.attend_qkv(self.qkv(x2, out=qkv_out), B, S, kv, out=out, workspace=workspace,
+                               pos_offset=pos_offset)
+
+    def attend_qkv(self, qkv, B, S, kv: LayerKV, out=None, workspace=None, pos_offset=0):
+        """RoPE, cache append and attention on an already computed q|k|v product."""
         H, Hk, D = self.local_num_heads, self.local_num_kv_heads, self.head_dim
-        qkv = self.qkv(x2, out=qkv_out)
-        cos_t, sin_t = self.rope.tables(kv.cache.capacity + pos_offset, x2.device)
+        cos_t, sin_t = self.rope.tables(kv.cache.capacity + pos_offset, qkv.device)
         _lib.rope_append_kv(qkv, B, S, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, pos_offset=pos_offset)
         return _lib.attention(qkv, B, S, H, Hk, D, kv.k, kv.vt, kv.counters, self.scale, out=out,
                               workspace=workspace)

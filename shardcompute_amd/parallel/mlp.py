@@ -91,6 +91,11 @@ class ParallelMLP:
         gu = self.gate_up(x2, out=gu_out)
         return _lib.silu_mul(gu, out=out)
 
+    async def down_from_gate_up(self, gate_up, act_out=None):
+        """down(silu(gate) * up) from the fused gate|up product."""
+        self._check_supported()
+        return await self.down_proj.forward(_lib.silu_mul(gate_up, out=act_out))
+
     async def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         lead = hidden_states.shape[:-1]
         a = self.intermediate(hidden_states.reshape(-1, self.hidden_size))

@@ -5,12 +5,14 @@ Drop-in for ``src/shardcompute/parallel/transformer.py``: ``RMSNorm``
 ``ParallelTransformer`` (``:339-596``) keep their constructor arguments,
 loaders, attributes and ``async forward`` signatures.
 
-``ParallelTransformer.forward`` runs the residual stream in place: each RMSNorm
-launch also performs the residual add that precedes it (``transformer.py:246,
-252``), so a layer is norm -> fused q|k|v product -> RoPE/KV append ->
-attention -> o_proj -> norm(+add) -> fused gate|up product -> SiLU gate ->
-down_proj, with no separate elementwise launches.  The same trunk is what the
-executor captures in a HIP graph for one decode step.
+``ParallelTransformer.forward`` runs a layer as four quantized products plus
+RoPE/append and attention: RMSNorm(h + pending) inside the fused q|k|v product,
+RoPE/KV append, attention, o_proj, RMSNorm(h + o) inside the fused gate|up
+product, and silu(gate) * up inside down_proj.  The residual adds of
+``transformer.py:246, 252`` ride in the norms, and the final norm rides in the
+lm_head.  At decode sizes each norm/gate is applied by the GEMV kernel while it
+stages its input rows, so there are no separate elementwise launches.  The same
+trunk is what the executor captures in a HIP graph for one decode step.
 
 Two keyword-only extensions select the embedding and lm_head formats of a
 measured workload without changing the reference defaults: ``embedding``
@@ -150,6 +152,7 @@ class StepBuffers:
         self.B, self.S = B, S
         self.ids = torch.zeros((B, S), dtype=torch.int32, device=dev)
         self.h = torch.empty((rows, model.hidden_size), dtype=bf, device=dev)
+        self.h2 = torch.empty_like(self.h)
         self.xn = torch.empty_like(self.h)
         self.qkv = torch.empty((rows, att.qkv_width), dtype=bf, device=dev)
         self.attn = torch.empty((rows, att.local_hidden), dtype=bf, device=dev)
@@ -278,22 +281,31 @@ class ParallelTransformer:
         return emb
 
     async def _trunk(self, h, cache: KVCache, B: int, S: int, bufs: Optional[StepBuffers] = None):
-        """Residual stream ``h [B*S, hidden]`` through every layer, updated in place.
+        """Residual stream ``h [B*S, hidden]`` through every layer.
 
-        Returns the last layer's MLP output (the residual add still pending)."""
+        Each RMSNorm (with the residual add before it) runs inside the projection
+        that reads it, and the SiLU gate inside down_proj.  The residual stream
+        alternates between two buffers (a kernel's h_out may not alias its input).
+        Returns (h, the last layer's MLP output whose residual add is pending)."""
+        h_alt = bufs.h2 if bufs is not None else torch.empty_like(h)
         pending = None
         for i, layer in enumerate(self.layers):
             att, mlp = layer.attention, layer.mlp
-            ln1, ln2 = layer.input_layernorm, layer.post_attention_layernorm
-            xn = ln1(h, residual=pending, h_out=h if pending is not None else None,
-                     out=bufs.xn if bufs is not None else None)
-            a = att.attend(xn, B, S, cache[i], out=bufs.attn if bufs else None, qkv_out=bufs.qkv if bufs else None,
-                           workspace=bufs.workspace if bufs else None)
+            qkv, _ = att.qkv.norm_call(h, layer.input_layernorm, residual=pending,
+                                       h_out=h_alt if pending is not None else None,
+                                       xn_out=bufs.xn if bufs is not None else None,
+                                       out=bufs.qkv if bufs is not None else None)
+            if pending is not None:
+                h, h_alt = h_alt, h
+            a = att.attend_qkv(qkv, B, S, cache[i], out=bufs.attn if bufs else None,
+                               workspace=bufs.workspace if bufs else None)
             o = await att.o_proj.forward(a)
-            xn = ln2(h, residual=o, h_out=h, out=bufs.xn if bufs is not None else None)
-            act = mlp.intermediate(xn, gu_out=bufs.gu if bufs else None, out=bufs.act if bufs else None)
-            pending = await mlp.down_proj.forward(act)
-        return pending
+            gu, _ = mlp.gate_up.norm_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
+                                          xn_out=bufs.xn if bufs is not None else None,
+                                          out=bufs.gu if bufs is not None else None)
+            h, h_alt = h_alt, h
+            pending = await mlp.down_from_gate_up(gu, act_out=bufs.act if bufs else None)
+        return h, pending
 
     async def _head(self, h, pending, B, S, last_only, hn_out=None):
         if pending is None:
@@ -301,6 +313,21 @@ class ParallelTransformer:
         if last_only and S > 1:
             h = h.reshape(B, S, -1)[:, -1].contiguous()
             pending = pending.reshape(B, S, -1)[:, -1].contiguous()
+        lm = self.lm_head
+        if isinstance(lm, QuantizedColumnParallelLinear):
+            if lm.quantized_weight is None:
+                raise RuntimeError("Weight not loaded")
+            self.norm._check()
+            # the final norm runs inside the lm_head kernel
+            logits, _ = _lib.qmm_rmsnorm(h, self.norm.weight, self.norm.eps, lm.quantized_weight, lm.scales,
+                                         lm.biases_quant, residual=pending, xn_out=hn_out,
+                                         bias=lm.bias if lm.has_bias else None, bits=lm.bits,
+                                         group_size=lm.group_size)
+            if lm.gather_output:
+                if self.communicator is None:
+                    raise RuntimeError("Communicator required for gather_output=True")
+                logits = await self.communicator.all_gather(logits, dim=-1)
+            return logits
         hn = self.norm(h, residual=pending, h_out=None, out=hn_out)
         if self.tie_word_embeddings:
             emb = self.embed_tokens
@@ -309,7 +336,7 @@ class ParallelTransformer:
             if self.communicator is not None:
                 logits = await self.communicator.all_gather(logits, dim=-1)
         else:
-            logits = await self.lm_head.forward(hn)
+            logits = await lm.forward(hn)
         return logits
 
     async def forward(self, input_ids, attention_mask=None, past_key_values=None, use_cache: bool = False, *,
@@ -335,7 +362,7 @@ class ParallelTransformer:
                 cache.load_tuples(past_key_values)
         cache.check_room(S)
         h = (await self._embed(ids)).reshape(B * S, self.hidden_size).contiguous()
-        pending = await self._trunk(h, cache, B, S)
+        h, pending = await self._trunk(h, cache, B, S)
         logits = await self._head(h, pending, B, S, last_only)
         cache.advance(S)
         new_cache = (cache.as_tuples() if tuples else cache) if use_cache else None
@@ -348,7 +375,7 @@ class ParallelTransformer:
         length and the step counter.  Captured once, replayed per token."""
         B = bufs.B
         h = self._embed_sync(bufs.ids, out=bufs.h.view(B, 1, self.hidden_size)).view(B, self.hidden_size)
-        pending = run_sync(self._trunk(h, cache, B, 1, bufs))
+        h, pending = run_sync(self._trunk(h, cache, B, 1, bufs))
         logits = run_sync(self._head(h, pending, B, 1, True, hn_out=bufs.hn))
         _lib.argmax(logits.reshape(B, -1), ids=bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
         _lib.add_i32(cache.counters, 1, n=2)

@@ -1,0 +1,79 @@
+"""The decode GEMV with the fused RMSNorm (+ residual) prologue against the
+standalone norm followed by the plain product, and against the oracle.
+
+The fused and unfused paths share the arithmetic and the row partition, and the
+GEMV's split-tile reduction is in a fixed order, so they agree bit for bit; the
+oracle comparison is at the linear tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_to_f32, f32_to_bf16
+from oracle.decoder import rms_norm
+from oracle.mlx_affine import quantize_bf16, quantized_matmul_f64
+from shardcompute_amd import _lib
+from tests.gpu_util import LINEAR_TOL, dev_bf16, dev_u32, host_u16, max_abs_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(rng, N, K, bits):
+    w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    return quantize_bf16(w, 64, bits)
+
+
+def _bf(rng, shape, scale=1.0):
+    return f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K,bits", [(1, 6144, 4096, 4), (3, 1000, 1024, 4), (8, 4096, 2048, 8),
+                                        (1, 520, 576, 4), (16, 512, 1024, 4), (1, 128256, 4096, 4)])
+def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
+    rng = np.random.default_rng(M * 31 + N + K)
+    wq, s, b = _weights(rng, N, K, bits)
+    x, r = _bf(rng, (M, K)), _bf(rng, (M, K))
+    nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    eps = 1e-5
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd, rd, nwd = dev_bf16(x), dev_bf16(r), dev_bf16(nw)
+    print(f"qmm_rmsnorm M={M} N={N} K={K} W{bits}", flush=True)
+    h = torch.empty_like(xd)
+    y, xn = _lib.qmm_rmsnorm(xd, nwd, eps, *W, residual=rd, h_out=h, bits=bits)
+    h2 = torch.empty_like(xd)
+    xn2 = _lib.rms_norm(xd, nwd, eps, residual=rd, h_out=h2)
+    y2 = _lib.qmm(xn2, *W, bits=bits)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(xn, xn2) and torch.equal(y, y2)
+    # without residual: no h_out written
+    y3, xn3 = _lib.qmm_rmsnorm(xd, nwd, eps, *W, bits=bits)
+    assert torch.equal(xn3, _lib.rms_norm(xd, nwd, eps))
+    # against the oracle
+    hr = f32_to_bf16(bf16_to_f32(x) + bf16_to_f32(r))
+    xnr = f32_to_bf16(rms_norm(bf16_to_f32(hr), nw, eps))
+    ref = quantized_matmul_f64(xnr, wq, s, b, 64, bits)
+    assert max_abs_rel(host_u16(y), ref) <= LINEAR_TOL
+
+
+def test_gemv_is_reproducible(device):
+    # tiles split between waves are summed in a fixed order: repeated launches agree
+    rng = np.random.default_rng(3)
+    for (N, K) in ((4096, 14336), (28672, 4096), (1000, 5120)):
+        wq, s, b = _weights(rng, N, K, 4)
+        W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+        x = dev_bf16(_bf(rng, (1, K)))
+        ys = [_lib.qmm(x, *W) for _ in range(5)]
+        torch.cuda.synchronize()
+        assert all(torch.equal(ys[0], y) for y in ys[1:]), (N, K)
+
+
+def test_fused_rejects_aliasing(device):
+    rng = np.random.default_rng(4)
+    wq, s, b = _weights(rng, 64, 512, 4)
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    x, r = dev_bf16(_bf(rng, (1, 512))), dev_bf16(_bf(rng, (1, 512)))
+    nw = dev_bf16(f32_to_bf16(np.ones(512, np.float32)))
+    with pytest.raises(RuntimeError, match="overlap"):
+        _lib.qmm_rmsnorm(x, nw, 1e-5, *W, residual=r, h_out=x)
+    with pytest.raises(RuntimeError, match="overlap"):
+        _lib.qmm_rmsnorm(x, nw, 1e-5, *W, residual=r, xn_out=r)
