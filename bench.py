@@ -116,8 +116,9 @@ def build_model(cfg, layers, bits, capacity, seed=0):
 
 def gemv_launches(model):
     """(name, prologue, wq, scales, biases, K, N) of every quantized product of one
-    decode step, with the input transformation its kernel applies: "norm" (RMSNorm
-    + residual add) or "" (plain)."""
+    decode step, with the transformations its kernel applies: "norm" (RMSNorm +
+    residual add on the input), "norm+swiglu" (and silu(gate) * up on paired output
+    columns) or "" (plain)."""
     out = []
     for layer in model.layers:
         att, mlp = layer.attention, layer.mlp
@@ -127,7 +128,7 @@ def gemv_launches(model):
         op = att.o_proj
         out.append(("o", "", op.quantized_weight, op.scales, op.biases_quant, op.local_in_features,
                     op.out_features))
-        out.append(("gate_up", "norm", gu._wq, gu._s, gu._b, K, gu.out_features))
+        out.append(("gate_up", "norm+swiglu", gu._wq, gu._s, gu._b, K, gu.out_features))
         dp = mlp.down_proj
         out.append(("down", "", dp.quantized_weight, dp.scales, dp.biases_quant, dp.local_in_features,
                     dp.out_features))
@@ -138,7 +139,8 @@ def gemv_launches(model):
 
 
 def qmm_bytes(M, N, K, bits):
-    """Algorithmic bytes of one quantized product: weights + bf16 scales/biases + x + y."""
+    """Algorithmic bytes of one quantized product: weights + bf16 scales/biases + x + y
+    (y counted at N columns; the gated gate|up product writes N / 2)."""
     return N * K * bits // 8 + N * (K // 64) * 2 * 2 + M * K * 2 + M * N * 2
 
 
@@ -152,14 +154,20 @@ def _gemv_io(launches, batch):
           "xn": {K: torch.empty((batch, K), dtype=torch.bfloat16, device=dev) for K in Ks},
           "nw": {K: torch.ones(K, dtype=torch.bfloat16, device=dev) for K in Ks},
           "gu": {K: torch.randn((batch, 2 * K), device=dev).to(torch.bfloat16) for K in Ks},
-          "y": {N: torch.empty((batch, N), dtype=torch.bfloat16, device=dev) for N in {l[6] for l in launches}}}
+          "y": {N: torch.empty((batch, N), dtype=torch.bfloat16, device=dev) for N in {l[6] for l in launches}},
+          "act": {N // 2: torch.empty((batch, N // 2), dtype=torch.bfloat16, device=dev)
+                  for N in {l[6] for l in launches}}}
     return io
 
 
 def _launch_all(launches, io, bits):
     from shardcompute_amd import _lib
     for name, pro, wq, s, b, K, N in launches:
-        if pro == "norm":
+        if pro == "norm+swiglu":
+            _lib.qmm_swiglu(io["x"][K], wq, s, b, norm_weight=io["nw"][K], eps=1e-5, residual=io["res"][K],
+                            h_out=io["h"][K], xn_out=io["xn"][K], bits=bits, act_out=io["act"][N // 2],
+                            gate_up_scratch=io["y"][N])
+        elif pro == "norm":
             _lib.qmm_rmsnorm(io["x"][K], io["nw"][K], 1e-5, wq, s, b, residual=io["res"][K], h_out=io["h"][K],
                              xn_out=io["xn"][K], bits=bits, out=io["y"][N])
         else:

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 3
+#define SC_ABI_VERSION 4
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -126,6 +126,24 @@ int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
                         uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
                         const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N,
                         int64_t K, int bits, int group_size, void *hip_stream);
+
+/*
+ * act = silu(gate) * up for the stacked gate|up weight wq [2I, K*bits/32] (gate rows
+ * first; scales/biases [2I, K/64], bias_or_null [2I]) applied to x, or to
+ * xn = RMSNorm(x + residual) when norm_weight_or_null is given (xn_out and, with a
+ * residual, h_out receive xn and x + residual as for sc_qmm_rmsnorm_bf16).  The
+ * decode GEMV (M <= 8) pairs gate row i with up row I + i inside one tile and writes
+ * act [M, I] directly; otherwise the product goes to gate_up_scratch [M, 2I] and
+ * the standalone sc_silu_mul_bf16 follows.  Outputs must not overlap the inputs.
+ * Replaces ParallelMLP.forward's gate/up projections and activation
+ * (src/shardcompute/parallel/mlp.py:241-245), after the post-attention layernorm
+ * (transformer.py:249-250).
+ */
+int sc_qmm_swiglu_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight_or_null,
+                       float eps, uint16_t *h_out_or_null, uint16_t *xn_out_or_null, const uint32_t *wq,
+                       const uint16_t *scales, const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *act_out,
+                       uint16_t *gate_up_scratch, int64_t M, int64_t I, int64_t K, int bits, int group_size,
+                       void *hip_stream);
 
 /* ------------------------------------------------------------------------------
  * Decoder wiring around the quantized linears.  The cache length (the number of

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -28,6 +28,7 @@ EXPORTS = (
     "sc_dequantize_bf16",
     "sc_quantize_affine",
     "sc_qmm_rmsnorm_bf16",
+    "sc_qmm_swiglu_bf16",
     "sc_rms_norm_bf16",
     "sc_rope_append_kv_bf16",
     "sc_attention_workspace_bytes",
@@ -79,6 +80,8 @@ def load():
         f32 = ctypes.c_float
         lib.sc_qmm_rmsnorm_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
         lib.sc_qmm_rmsnorm_bf16.restype = i32
+        lib.sc_qmm_swiglu_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
+        lib.sc_qmm_swiglu_bf16.restype = i32
         lib.sc_rms_norm_bf16.argtypes = [p, p, p, p, p, i64, i64, f32, p]
         lib.sc_rms_norm_bf16.restype = i32
         lib.sc_rope_append_kv_bf16.argtypes = [p, i64, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, p]
@@ -226,6 +229,43 @@ def qmm_rmsnorm(x, norm_weight, eps, wq, scales, biases, residual=None, h_out=No
                                  group_size, _stream(x))
     _check(rc, "sc_qmm_rmsnorm_bf16")
     return y.reshape(*lead, N), xn.reshape(*lead, K)
+
+
+def qmm_swiglu(x, wq, scales, biases, norm_weight=None, eps=1e-5, residual=None, h_out=None, xn_out=None,
+               bias=None, bits=4, group_size=64, act_out=None, gate_up_scratch=None):
+    """act = silu(gate) * up for the stacked gate|up weight [2I, ...] applied to x,
+    or to RMSNorm(x + residual) when ``norm_weight`` is given.  Returns (act, xn)."""
+    lib = load()
+    _require_gpu(x, wq, scales, biases, norm_weight, residual, h_out, xn_out, bias, act_out, gate_up_scratch)
+    K = x.shape[-1]
+    _rows(x, K, "x")
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    wq, scales, biases, bias, N = _qmm_common(wq, scales, biases, bias, bits, group_size, K)
+    if N % 16:
+        raise ValueError(f"gate|up rows ({N}) must be 2 * I with I a multiple of 8")
+    I = N // 2
+    xn = None
+    if norm_weight is not None:
+        if norm_weight.shape != (K,) or norm_weight.dtype != torch.bfloat16:
+            raise ValueError(f"norm weight must be bf16 [{K}]")
+        xn = xn_out if xn_out is not None else torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+        _rows(xn, K, "xn_out")
+        norm_weight = norm_weight.contiguous()
+    elif residual is not None:
+        raise ValueError("a residual needs the norm weight")
+    if residual is not None:
+        _rows(residual, K, "residual")
+    act = act_out if act_out is not None else torch.empty((M, I), dtype=torch.bfloat16, device=x.device)
+    _rows(act, I, "act_out")
+    gu = gate_up_scratch if gate_up_scratch is not None else torch.empty((M, N), dtype=torch.bfloat16,
+                                                                          device=x.device)
+    _rows(gu, N, "gate_up_scratch")
+    rc = lib.sc_qmm_swiglu_bf16(_ptr(x), _ptr(residual), _ptr(norm_weight), float(eps), _ptr(h_out), _ptr(xn),
+                                _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(act), _ptr(gu), M, I, K, bits,
+                                group_size, _stream(x))
+    _check(rc, "sc_qmm_swiglu_bf16")
+    return act.reshape(*lead, I), (xn.reshape(*lead, K) if xn is not None else None)
 
 
 def vocab_gather(ids, table, vocab_start=0, out=None):

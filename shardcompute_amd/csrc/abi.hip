@@ -169,36 +169,58 @@ static bool overlap(const void *a, size_t an, const void *b, size_t bn) {
     return x < y + bn && y < x + an;
 }
 
-// The quantized product of a normalised input: RMSNorm of x (+ res).  The decode
-// GEMV applies the norm while staging its rows; otherwise the standalone kernel
-// writes x_out and the product reads it.  Either way x_out (and h_out) hold the
-// staged rows afterwards.
-static int qmm_fused(int kind, const uint16_t *x, const uint16_t *res, const uint16_t *nw, float eps,
-                     uint16_t *h_out, uint16_t *x_out, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
-                     const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits, int group_size,
-                     void *stream) {
-    const char *what = "qmm_rmsnorm";
-    int rc = check_qmm(x_out, wq, s, b, y, M, N, K, bits, group_size);
+// The quantized product of a transformed input and/or with a transformed output:
+//  * nw != null: the input is RMSNorm(x + res) (res optional), left in x_out and,
+//    with res, x + res in h_out;
+//  * swiglu_half > 0: the weight is gate|up stacked [2I, K] and y receives
+//    act = silu(gate) * up [M, I] (gu_scratch [M, 2I] holds the product when the
+//    fused kernel does not apply).
+// The decode GEMV applies both while staging its rows / writing its tiles;
+// otherwise the standalone kernels run around the plain product.
+static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw, float eps, uint16_t *h_out,
+                     uint16_t *x_out, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
+                     uint16_t *y, int64_t M, int64_t N, int64_t K, int bits, int group_size, void *stream,
+                     int64_t swiglu_half, uint16_t *gu_scratch) {
+    const char *what = swiglu_half ? "qmm_swiglu" : "qmm_rmsnorm";
+    const uint16_t *xin = nw ? x_out : x;
+    int rc = check_qmm(xin, wq, s, b, y, M, N, K, bits, group_size);
     if (rc) return rc;
-    if (!x || !nw) return set_error(SC_EINVAL, "%s: null pointer argument", what);
+    if (!x) return set_error(SC_EINVAL, "%s: null pointer argument", what);
+    if (!nw && res) return set_error(SC_EINVAL, "%s: a residual needs the norm weight", what);
     if (K % 8) return set_error(SC_EINVAL, "%s: K=%lld must be a multiple of 8", what, (long long)K);
     if (!aligned(x, 16) || !aligned(res, 16) || !aligned(nw, 16) || !aligned(h_out, 16))
         return set_error(SC_EINVAL, "%s: activation pointers must be 16-byte aligned", what);
-    const size_t row_bytes = (size_t)M * K * 2, in_bytes = row_bytes;
-    if (overlap(x_out, row_bytes, x, in_bytes) || overlap(x_out, row_bytes, res, row_bytes) ||
-        overlap(h_out, row_bytes, x, in_bytes) || overlap(h_out, row_bytes, res, row_bytes) ||
-        overlap(h_out, row_bytes, x_out, row_bytes))
-        return set_error(SC_EINVAL, "%s: outputs must not overlap the inputs (other workgroups still read them)",
-                         what);
+    const int64_t n_out = swiglu_half ? swiglu_half : N;
+    if (swiglu_half) {
+        if (swiglu_half % 8 || N != 2 * swiglu_half)
+            return set_error(SC_EINVAL, "%s: the weight must stack gate and up ([2I, K]) with I a multiple of 8", what);
+        if (!gu_scratch || !aligned(gu_scratch, 16)) return set_error(SC_EINVAL, "%s: gate_up scratch required", what);
+    }
+    const size_t xb = (size_t)M * K * 2, yb = (size_t)M * n_out * 2, gb = (size_t)M * N * 2;
+    const void *outs[4] = {x_out, h_out, y, gu_scratch};
+    const size_t outb[4] = {xb, xb, yb, gb};
+    for (int i = 0; i < 4; ++i) {
+        if (overlap(outs[i], outb[i], x, xb) || overlap(outs[i], outb[i], res, xb))
+            return set_error(SC_EINVAL, "%s: outputs must not overlap the inputs (other workgroups still read them)",
+                             what);
+        for (int k = 0; k < i; ++k)
+            if (overlap(outs[i], outb[i], outs[k], outb[k]))
+                return set_error(SC_EINVAL, "%s: output buffers overlap", what);
+    }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (qgemv_dma_eligible(x_out, wq, s, b, (int)M, (int)K)) {
-        DmaFused f{kind, res, nw, eps, h_out, x_out};
+    if (qgemv_dma_eligible(xin, wq, s, b, (int)M, (int)K)) {
+        DmaFused f{nw ? PRO_NORM_KIND : 0, (int)swiglu_half, res, nw, eps, res ? h_out : nullptr, x_out};
         rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, &f);
         if (rc != SC_EUNSUPPORTED) return rc;
     }
-    rc = launch_rms_norm(x, res, nw, x_out, h_out, M, K, eps, st);
+    if (nw) {
+        rc = launch_rms_norm(x, res, nw, x_out, res ? h_out : nullptr, M, K, eps, st);
+        if (rc) return rc;
+    }
+    if (!swiglu_half) return qmm_dispatch(xin, wq, s, b, bias, y, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
+    rc = qmm_dispatch(xin, wq, s, b, bias, gu_scratch, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
     if (rc) return rc;
-    return qmm_dispatch(x_out, wq, s, b, bias, y, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
+    return launch_silu_mul(gu_scratch, M, swiglu_half, y, st);
 }
 
 }  // namespace sc
@@ -321,8 +343,19 @@ int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
                         uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
                         const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N,
                         int64_t K, int bits, int group_size, void *hip_stream) {
-    return qmm_fused(PRO_NORM_KIND, x, residual_or_null, norm_weight, eps, residual_or_null ? h_out_or_null : nullptr,
-                     xn_out, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream);
+    if (!norm_weight || !xn_out) return set_error(SC_EINVAL, "qmm_rmsnorm: null pointer argument");
+    return qmm_fused(x, residual_or_null, norm_weight, eps, h_out_or_null, xn_out, wq, scales, biases, bias_or_null, y,
+                     M, N, K, bits, group_size, hip_stream, 0, nullptr);
+}
+
+int sc_qmm_swiglu_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight_or_null,
+                       float eps, uint16_t *h_out_or_null, uint16_t *xn_out_or_null, const uint32_t *wq,
+                       const uint16_t *scales, const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *act_out,
+                       uint16_t *gate_up_scratch, int64_t M, int64_t I, int64_t K, int bits, int group_size,
+                       void *hip_stream) {
+    if (norm_weight_or_null && !xn_out_or_null) return set_error(SC_EINVAL, "qmm_swiglu: xn_out required with a norm");
+    return qmm_fused(x, residual_or_null, norm_weight_or_null, eps, h_out_or_null, xn_out_or_null, wq, scales, biases,
+                     bias_or_null, act_out, M, 2 * I, K, bits, group_size, hip_stream, I, gate_up_scratch);
 }
 
 

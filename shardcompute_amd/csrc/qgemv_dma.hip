@@ -36,6 +36,14 @@ enum DmaPrologue {
                     // post-attention layernorm before gate|up, the final norm before the lm_head
 };
 
+// What the kernel does with its output columns.
+enum DmaEpilogue {
+    EPI_NONE = 0,   // y [M, N]
+    EPI_SWIGLU = 1, // the weight is gate|up stacked ([2I, K]); tile t pairs gate rows
+                    // 8t..8t+7 with up rows I+8t..I+8t+7 and writes act = silu(g) * u
+                    // [M, I] (parallel/mlp.py:241-245), never g and u themselves
+};
+
 struct DmaArgs {
     const uint16_t *x;
     const uint32_t *wq;
@@ -52,6 +60,7 @@ struct DmaArgs {
     uint16_t *h_out;        // PRO_NORM with res: x + res, written by workgroup 0
     uint16_t *x_out;        // the staged input rows (normalised / gated), written by workgroup 0
     int dma_stage;          // input rows are staged by LDS-DMA (they fit the staging areas)
+    int half;               // EPI_SWIGLU: I (rows of the gate half, output width)
 };
 
 namespace {
@@ -125,7 +134,7 @@ __device__ __forceinline__ void wait_vm() {
 
 // MR: 1 for a single row of x (only D register 0 of lane-groups 0 and 2 matters),
 // 8 for up to 8 rows.
-template <int BITS, int MR, int PRO>
+template <int BITS, int MR, int PRO, int EPI>
 __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a) {
     constexpr int NR = MR == 1 ? 1 : 4;                // D registers that can hold a row < M
     constexpr int SPAN_K = BITS == 4 ? 128 : 64;       // one 64-byte span of a row
@@ -180,15 +189,20 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
     int iss_tl = lo / CPT, iss_ch = lo - (lo / CPT) * CPT, iss_left = hi - lo;
     const uint8_t *gw[4];
     const uint16_t *gsb = nullptr;
+    // weight row of row r (0..15) of the tile that starts at output column n0
+    auto wrow = [&](int n0, int r) -> int {
+        if (EPI == EPI_SWIGLU) return (r < 8 ? 0 : a.half - 8) + (n0 >> 1) + r;
+        return min(n0 + r, N - 1);
+    };
     auto set_tile = [&](int tl) {
         const int n0 = (t_begin + tl) * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 4 * i + (lane >> 4);
             const int col = ((lane & 15) - r) & 15;
-            gw[i] = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)min(n0 + r, N - 1) * row_bytes + col * 16;
+            gw[i] = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)wrow(n0, r) * row_bytes + col * 16;
         }
-        gsb = (lane < 16 ? a.s : a.b) + (size_t)min(n0 + j, N - 1) * G;
+        gsb = (lane < 16 ? a.s : a.b) + (size_t)wrow(n0, j) * G;
     };
     set_tile(iss_tl);
     auto issue = [&](int slot) {
@@ -365,7 +379,7 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
     }
     if (a.bias)
         for (int idx = tid; idx < ntl * 16; idx += blockDim.x)
-            bias_l[idx] = a.bias[min(t_begin * 16 + idx, N - 1)];
+            bias_l[idx] = a.bias[wrow((t_begin + (idx >> 4)) * 16, idx & 15)];
     for (int idx = tid; idx < W; idx += blockDim.x) xl[M * xstride + idx] = make_uint4(0u, 0u, 0u, 0u);
     for (int idx = tid; idx < ntl; idx += blockDim.x) cnt[idx] = 0;
     __syncthreads();
@@ -405,6 +419,17 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
             a.y[(size_t)m * N + nn] = (uint16_t)o;
         }
     };
+    // gate (jg) and up (jg + 8) columns of a paired tile -> act column 8 * tile + jg
+    auto write_act = [&](int tl, int m, int jg, float vg, float vu) {
+        if (m < M) {
+            uint32_t gb = f2bf(vg), ub = f2bf(vu);
+            if (a.bias) {
+                gb = f2bf(bf2f(gb) + bf2f(bias_l[tl * 16 + jg]));
+                ub = f2bf(bf2f(ub) + bf2f(bias_l[tl * 16 + 8 + jg]));
+            }
+            a.y[(size_t)m * a.half + (size_t)(t_begin + tl) * 8 + jg] = (uint16_t)f2bf(silu_mul_f(bf2f(gb), bf2f(ub)));
+        }
+    };
     int fin_a = -1, fin_b = -1;      // split tiles this wave completes
     auto flush = [&]() {
         f4 fin = acc;
@@ -413,7 +438,15 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
             for (int r = 0; r < 4; ++r) fin[r] += __shfl_xor(fin[r], 32);
         }
         if (chunks_in_acc == CPT) {
-            if (q < 2) {
+            if (EPI == EPI_SWIGLU) {
+                f4 up;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(fin[r], 8);   // column j + 8 of the same rows
+                if (q < 2 && j < 8) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) write_act(cur_tile, em0 + r, j, fin[r], up[r]);
+                }
+            } else if (q < 2) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) write_out(cur_tile, em0 + r, j, fin[r]);
             }
@@ -532,14 +565,20 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
         if (tile < 0) continue;
         wait_lgkm0();
         const int ts = tile * CPT, te = ts + CPT;
-        for (int o = lane; o < M * 16; o += 64) {
+        auto slot_sum = [&](int o) {
             float v = 0.f;
             for (int w2 = 0; w2 < nwaves; ++w2) {
                 const int lo2 = (w2 * items) >> nwl2, hi2 = ((w2 + 1) * items) >> nwl2;
                 if (hi2 <= lo2 || hi2 <= ts || lo2 >= te) continue;
                 v += part_l[((size_t)w2 * 2 + (lo2 / CPT == tile ? 0 : 1)) * M * 16 + o];
             }
-            write_out(tile, o >> 4, o & 15, v);
+            return v;
+        };
+        if (EPI == EPI_SWIGLU) {
+            for (int o = lane; o < M * 8; o += 64)
+                write_act(tile, o >> 3, o & 7, slot_sum((o >> 3) * 16 + (o & 7)), slot_sum((o >> 3) * 16 + 8 + (o & 7)));
+        } else {
+            for (int o = lane; o < M * 16; o += 64) write_out(tile, o >> 4, o & 15, slot_sum(o));
         }
     }
 }
@@ -582,9 +621,16 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
     a.M = M; a.N = N; a.K = K; a.G = G; a.max_tiles_per_block = max_tpb;
     a.pro = PRO_NONE; a.res = nullptr; a.nw = nullptr; a.eps = 0.f; a.h_out = nullptr; a.x_out = nullptr;
+    a.half = 0;
+    int epi = EPI_NONE;
     if (fused) {
         a.pro = fused->kind; a.res = fused->res; a.nw = fused->norm_weight; a.eps = fused->eps;
         a.h_out = fused->h_out; a.x_out = fused->x_out;
+        if (fused->swiglu_half > 0) {
+            if (fused->swiglu_half % 8 || N != 2 * fused->swiglu_half) return SC_EUNSUPPORTED;
+            epi = EPI_SWIGLU;
+            a.half = fused->swiglu_half;
+        }
     }
     {
         // LDS-DMA staging needs 16-byte rows, the raw rows within the x area, the
@@ -612,24 +658,26 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
         SC_HIP_CHECK(hipGetLastError());
         return SC_OK;
     };
-    // one instantiation per prologue keeps each kernel's code short (these launches
-    // are latency-bound, and a cold instruction fetch of unused prologue code shows)
-    static int cfg[2][2][2] = {};
+    // one instantiation per prologue and epilogue keeps each kernel's code short
+    // (these launches are latency-bound, and a cold instruction fetch of unused code
+    // shows)
+    static int cfg[2][2][2][2] = {};
     const int bi = bits == 4 ? 0 : 1, mi = M == 1 ? 0 : 1, pi = a.pro;
+    int &c = cfg[bi][mi][pi][epi];
+#define SC_DMA_PICK(B_, M_)                                                                        \
+    do {                                                                                            \
+        if (pi == PRO_NORM && epi == EPI_SWIGLU) return launch(qgemv_dma_kernel<B_, M_, PRO_NORM, EPI_SWIGLU>, c); \
+        if (pi == PRO_NORM) return launch(qgemv_dma_kernel<B_, M_, PRO_NORM, EPI_NONE>, c);        \
+        if (epi == EPI_SWIGLU) return launch(qgemv_dma_kernel<B_, M_, PRO_NONE, EPI_SWIGLU>, c);   \
+        return launch(qgemv_dma_kernel<B_, M_, PRO_NONE, EPI_NONE>, c);                            \
+    } while (0)
     if (bits == 4) {
-        if (M == 1) {
-            if (pi == PRO_NORM) return launch(qgemv_dma_kernel<4, 1, PRO_NORM>, cfg[bi][mi][pi]);
-            return launch(qgemv_dma_kernel<4, 1, PRO_NONE>, cfg[bi][mi][pi]);
-        }
-        if (pi == PRO_NORM) return launch(qgemv_dma_kernel<4, 8, PRO_NORM>, cfg[bi][mi][pi]);
-        return launch(qgemv_dma_kernel<4, 8, PRO_NONE>, cfg[bi][mi][pi]);
+        if (M == 1) SC_DMA_PICK(4, 1);
+        SC_DMA_PICK(4, 8);
     }
-    if (M == 1) {
-        if (pi == PRO_NORM) return launch(qgemv_dma_kernel<8, 1, PRO_NORM>, cfg[bi][mi][pi]);
-        return launch(qgemv_dma_kernel<8, 1, PRO_NONE>, cfg[bi][mi][pi]);
-    }
-    if (pi == PRO_NORM) return launch(qgemv_dma_kernel<8, 8, PRO_NORM>, cfg[bi][mi][pi]);
-    return launch(qgemv_dma_kernel<8, 8, PRO_NONE>, cfg[bi][mi][pi]);
+    if (M == 1) SC_DMA_PICK(8, 1);
+    SC_DMA_PICK(8, 8);
+#undef SC_DMA_PICK
 }
 
 }  // namespace sc

@@ -90,19 +90,16 @@ __device__ __forceinline__ uint4 norm_bf16x8(uint4 h, uint4 w, float root) {
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// bf16((g / (1 + exp(-g))) * u) (parallel/mlp.py:161-162, 244)
+// (g / (1 + exp(-g))) * u in fp32 (parallel/mlp.py:161-162, 244)
+__device__ __forceinline__ float silu_mul_f(float g, float u) {
+    return mul_rn(__fdiv_rn(g, add_rn(1.f, expf(-g))), u);
+}
+
+// bf16(silu(g) * u), 8 packed bf16
 __device__ __forceinline__ uint4 silu_mul_bf16x8(uint4 g, uint4 u) {
     uint32_t o[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        float r[2];
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const float gg = bfe(g, 2 * e + k);
-            r[k] = mul_rn(__fdiv_rn(gg, add_rn(1.f, expf(-gg))), bfe(u, 2 * e + k));
-        }
-        o[e] = pack_bf16x2(r[0], r[1]);
-    }
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(silu_mul_f(bfe(g, 2 * e), bfe(u, 2 * e)), silu_mul_f(bfe(g, 2 * e + 1), bfe(u, 2 * e + 1)));
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
@@ -178,6 +175,7 @@ int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out)
 // qgemv_dma.hip): 1 = RMSNorm of x (+ res), 2 = silu(gate) * up of x = gate|up.
 struct DmaFused {
     int kind;
+    int swiglu_half;     // > 0: paired gate|up tiles, output act [M, swiglu_half]
     const uint16_t *res;
     const uint16_t *norm_weight;
     float eps;

@@ -107,5 +107,24 @@ class FusedColumns:
         xn = _lib.rms_norm(h, norm.weight, norm.eps, residual=residual, h_out=h_out, out=xn_out)
         return self(xn, out=out), xn
 
+    def swiglu_call(self, h, norm=None, residual=None, h_out=None, xn_out=None, act_out=None, gu_out=None):
+        """silu(gate) * up for a gate|up stack, of ``norm(h + residual)`` when a norm is
+        given: the quantized kernel pairs each gate column with its up column and
+        writes the gated activation directly.  Returns act."""
+        if not self._current():
+            self.build()
+        if len(self.parts) != 2 or self.widths[0] != self.widths[1]:
+            raise ValueError("swiglu needs a gate|up pair of equal widths")
+        if norm is not None:
+            norm._check()
+        if self.quantized:
+            act, _ = _lib.qmm_swiglu(h, self._wq, self._s, self._b, norm_weight=norm.weight if norm else None,
+                                     eps=norm.eps if norm else 1e-5, residual=residual, h_out=h_out,
+                                     xn_out=xn_out, bias=self._bias, bits=self.bits, group_size=self.group_size,
+                                     act_out=act_out, gate_up_scratch=gu_out)
+            return act
+        xn = _lib.rms_norm(h, norm.weight, norm.eps, residual=residual, h_out=h_out, out=xn_out) if norm else h
+        return _lib.silu_mul(self(xn, out=gu_out), out=act_out)
+
     def split(self, y):
         return torch.split(y, self.widths, dim=-1)

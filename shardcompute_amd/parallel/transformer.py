@@ -8,7 +8,8 @@ loaders, attributes and ``async forward`` signatures.
 ``ParallelTransformer.forward`` runs a layer as four quantized products plus
 RoPE/append and attention: RMSNorm(h + pending) inside the fused q|k|v product,
 RoPE/KV append, attention, o_proj, RMSNorm(h + o) inside the fused gate|up
-product, and silu(gate) * up inside down_proj.  The residual adds of
+product whose kernel also applies silu(gate) * up to paired columns, and
+down_proj.  The residual adds of
 ``transformer.py:246, 252`` ride in the norms, and the final norm rides in the
 lm_head.  At decode sizes each norm/gate is applied by the GEMV kernel while it
 stages its input rows, so there are no separate elementwise launches.  The same
@@ -300,11 +301,13 @@ class ParallelTransformer:
             a = att.attend_qkv(qkv, B, S, cache[i], out=bufs.attn if bufs else None,
                                workspace=bufs.workspace if bufs else None)
             o = await att.o_proj.forward(a)
-            gu, _ = mlp.gate_up.norm_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
+            mlp._check_supported()
+            act = mlp.gate_up.swiglu_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
                                           xn_out=bufs.xn if bufs is not None else None,
-                                          out=bufs.gu if bufs is not None else None)
+                                          act_out=bufs.act if bufs is not None else None,
+                                          gu_out=bufs.gu if bufs is not None else None)
             h, h_alt = h_alt, h
-            pending = await mlp.down_from_gate_up(gu, act_out=bufs.act if bufs else None)
+            pending = await mlp.down_proj.forward(act)
         return h, pending
 
     async def _head(self, h, pending, B, S, last_only, hn_out=None):

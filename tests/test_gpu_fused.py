@@ -1,9 +1,14 @@
-"""The decode GEMV with the fused RMSNorm (+ residual) prologue against the
-standalone norm followed by the plain product, and against the oracle.
+"""The decode GEMV with a fused RMSNorm (+ residual) prologue and/or SwiGLU
+epilogue against the standalone kernels around the plain product, and against
+the oracle.
 
-The fused and unfused paths share the arithmetic and the row partition, and the
-GEMV's split-tile reduction is in a fixed order, so they agree bit for bit; the
-oracle comparison is at the linear tolerance.
+The norm prologue shares the arithmetic and row partition of the standalone
+norm and keeps the product's tiling, and the GEMV sums split tiles in a fixed
+order, so the norm-fused product agrees bit for bit.  The SwiGLU epilogue pairs
+gate and up columns in one tile, which changes where the k-sum splits between
+waves, so it agrees to rounding (a few elements move by a bf16 step of g or u); both are
+checked against the
+oracle at the linear tolerance.
 """
 import numpy as np
 import pytest
@@ -13,7 +18,7 @@ from oracle.bf16 import bf16_to_f32, f32_to_bf16
 from oracle.decoder import rms_norm
 from oracle.mlx_affine import quantize_bf16, quantized_matmul_f64
 from shardcompute_amd import _lib
-from tests.gpu_util import LINEAR_TOL, dev_bf16, dev_u32, host_u16, max_abs_rel
+from tests.gpu_util import LINEAR_TOL, bf16_ulp_diff, dev_bf16, dev_u32, host_u16, max_abs_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -53,6 +58,41 @@ def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
     xnr = f32_to_bf16(rms_norm(bf16_to_f32(hr), nw, eps))
     ref = quantized_matmul_f64(xnr, wq, s, b, 64, bits)
     assert max_abs_rel(host_u16(y), ref) <= LINEAR_TOL
+
+
+@pytest.mark.parametrize("M,I,K,bits,norm", [(1, 14336, 4096, 4, True), (1, 5632, 2048, 4, False),
+                                              (3, 1024, 1024, 8, True), (12, 512, 1024, 4, True),
+                                              (1, 2048, 576, 4, True)])
+def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
+    rng = np.random.default_rng(M * 7 + I + K)
+    wq, s, b = _weights(rng, 2 * I, K, bits)
+    x, r = _bf(rng, (M, K)), _bf(rng, (M, K))
+    nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd, rd, nwd = dev_bf16(x), dev_bf16(r), dev_bf16(nw)
+    print(f"qmm_swiglu M={M} I={I} K={K} W{bits} norm={norm}", flush=True)
+    if norm:
+        h = torch.empty_like(xd)
+        act, xn = _lib.qmm_swiglu(xd, *W, norm_weight=nwd, residual=rd, h_out=h, bits=bits)
+        h2 = torch.empty_like(xd)
+        xn2 = _lib.rms_norm(xd, nwd, 1e-5, residual=rd, h_out=h2)
+        assert torch.equal(h, h2) and torch.equal(xn, xn2)
+    else:
+        act, _ = _lib.qmm_swiglu(xd, *W, bits=bits)
+        xn2 = xd
+    act2 = _lib.silu_mul(_lib.qmm(xn2, *W, bits=bits))
+    torch.cuda.synchronize()
+    # the paired gate|up tiles split the k-sum between waves at other points than the
+    # plain product's tiles, so the fp32 sums may round differently: a rare element
+    # moves by a bf16 step of g or u (measured relative to the output's scale)
+    a1, a2 = host_u16(act), host_u16(act2)
+    assert max_abs_rel(a1, a2) <= 2e-3 and (bf16_ulp_diff(a1, a2) > 0).mean() < 0.02
+    xin = host_u16(xn2)
+    gu = quantized_matmul_f64(xin, wq, s, b, 64, bits)
+    g = bf16_to_f32(f32_to_bf16(gu[:, :I].astype(np.float32)))
+    u = bf16_to_f32(f32_to_bf16(gu[:, I:].astype(np.float32)))
+    ref = bf16_to_f32(f32_to_bf16((g / (np.float32(1) + np.exp(-g, dtype=np.float32))) * u))
+    assert max_abs_rel(host_u16(act), ref) <= LINEAR_TOL
 
 
 def test_gemv_is_reproducible(device):
