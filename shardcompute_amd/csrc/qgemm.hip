@@ -1,18 +1,26 @@
-// Kernel B: LDS-staged dequant -> bf16 MFMA GEMM for prefill-sized batches.
+// Kernel B: dequant -> bf16 MFMA GEMM for prefill-sized batches.
 //
-// Same contraction as kernel A (mx.quantized_matmul(..., transpose=True),
-// src/shardcompute/parallel/quantized_linear.py:168-176), for M >= 64 rows of x:
+// Same contraction as the decode GEMV (mx.quantized_matmul(..., transpose=True),
+// src/shardcompute/parallel/quantized_linear.py:168-176), for larger M:
 //     y[m, n] = sum_k x[m, k] * (s[n, k/64] * q[n, k] + b[n, k/64])
 //
-// Workgroup tile BM x BN, stepping K one quantization group (64) at a time.
-// Per step every thread issues its global loads for the next group (x tile
-// rows, packed weight bytes, one scale/bias pair) before the MFMAs of the
-// current group run; the weights are dequantized in registers to
-// bf16(s * q + b) and written, with the x tile, into the other half of a
-// double-buffered LDS area.  Waves (2 x 2) each own a (BM/2) x (BN/2) sub-tile
-// computed with v_mfma_f32_32x32x16_bf16, fp32 accumulation; the epilogue rounds
-// to bf16 and adds the optional linear bias after that rounding (the reference
-// adds the bias to the bf16 matmul result, quantized_linear.py:179-180).
+// * Workgroup tile 256 (m) x BN (n, 256 or 128), 8 waves in a 2 x 4 grid, each wave
+//   128 x BN/4 on v_mfma_f32_32x32x16_bf16 (fp32 accumulators).
+// * K advances one quantization group (64) per stage.  LDS holds two stages of the
+//   x tile and of the dequantized weight tile (rows of 128 bytes, 16-byte chunks
+//   swizzled by row & 7 so the MFMA operand reads spread over the banks).
+// * Loads run ahead of use: the packed weights, scales and biases two stages
+//   ahead (two register sets, so the stage loop is unrolled by two), the x tile one
+//   stage ahead.  During stage g's MFMAs each thread dequantizes its part of stage
+//   g+1's weights, a quarter per 16-k step, to bf16(s * q + b) (one fp32 FMA per
+//   weight, the reference's dequant) and stores it into the other weight buffer;
+//   the x rows of stage g+1 follow after the MFMAs, then one barrier per stage.
+// * The grid is ordered so that the workgroups sharing the x rows of one m-tile
+//   run on one XCD (workgroups are dealt to the 8 XCDs round robin), which keeps
+//   the x tiles in that XCD's L2; the packed weights stream from HBM.
+// * The epilogue rounds to bf16 and adds the optional linear bias after that
+//   rounding (the reference adds it to the bf16 matmul result,
+//   quantized_linear.py:179-180).
 #include "sc_common.h"
 
 namespace sc {
@@ -25,147 +33,218 @@ struct GemmArgs {
     const uint16_t *bias;
     uint16_t *y;
     int M, N, K, G;
+    int mt, nt, tiles;     // m-tiles, n-tiles, real tiles (the grid is padded to a multiple of 8)
 };
 
 namespace {
 
-constexpr int BM = 128;
-constexpr int BN = 128;
-constexpr int BK = 64;                 // one quantization group
-constexpr int ROW_U4 = BK * 2 / 16 + 1;  // 8 uint4 of bf16 per row + 1 pad
-constexpr int TILE_U4 = BM * ROW_U4;     // A tile (BM rows) == B tile (BN rows)
-constexpr int THREADS = 256;
+constexpr int BM = 256;
+constexpr int BK = 64;                    // one quantization group
+constexpr int THREADS = 512;
+constexpr int ROW_BYTES = BK * 2;         // 128 B of bf16 per tile row
+constexpr int XTILE = BM * ROW_BYTES;     // 32 KB
+constexpr int XCDS = 8;
 
-template <int BITS>
-struct WLoad {
-    uint4 v[BITS / 4];   // codes for 32 k of one row (W4: 16 B, W8: 32 B)
+template <int BN>
+struct Geo {
+    static constexpr int WTILE = BN * ROW_BYTES;                 // dequantized weight tile
+    static constexpr int STAGE = XTILE + WTILE;
+    static constexpr int LDS = 2 * STAGE;
+    static constexpr int WN = BN / 4;                            // wave tile width
+    static constexpr int NJ = WN / 32;                           // 32-column MFMA blocks per wave
+    static constexpr int TPR = THREADS / BN;                     // threads per weight row (2 or 4)
+    static constexpr int CPT = BK / TPR;                         // codes per thread and stage (32 or 16)
+};
+
+// swizzled byte offset of 16-byte chunk c of tile row r
+__device__ __forceinline__ uint32_t swz(int r, int c) { return (uint32_t)(r * ROW_BYTES + ((c ^ (r & 7)) << 4)); }
+
+template <int BITS, int CPT>
+struct WRegs {
+    uint32_t w[CPT * BITS / 32];   // this thread's codes of one row and stage
+    uint32_t s, b;
 };
 
 }  // namespace
 
-template <int BITS>
+template <int BITS, int BN>
 __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
+    using Gm = Geo<BN>;
+    constexpr int CPT = Gm::CPT;
+    constexpr int NW = CPT * BITS / 32;          // code words per thread and stage
     extern __shared__ __align__(16) uint8_t smem[];
-    uint4 *As = reinterpret_cast<uint4 *>(smem);   // [2][BM][ROW_U4]
-    uint4 *Bs = As + 2 * TILE_U4;                  // [2][BN][ROW_U4]
-
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * BN;
+    const int wm = wave >> 2, wn = wave & 3;
     const int M = a.M, N = a.N, K = a.K, G = a.G;
 
-    // x tile: 128 rows x 8 uint4 = 1024 uint4, 4 per thread
-    const uint16_t *xrow[4];
-    int xr[4], xc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int idx = tid + THREADS * i;
-        xr[i] = idx >> 3;
-        xc[i] = idx & 7;
-        xrow[i] = a.x + (size_t)min(m0 + xr[i], M - 1) * K + xc[i] * 8;
-    }
-    // weights: thread -> (row, half): 32 k of one row per group
-    const int wr = tid >> 1;
-    const int wh = tid & 1;
-    const int wn_row = min(n0 + wr, N - 1);
-    const uint4 *wbase = reinterpret_cast<const uint4 *>(a.wq) + (size_t)wn_row * ((size_t)K * BITS / 128);
-    const uint16_t *srow = a.s + (size_t)wn_row * G;
-    const uint16_t *brow = a.b + (size_t)wn_row * G;
+    // XCD-aware tile order: workgroup w runs on XCD w % 8; XCD x takes the tiles
+    // [x * per, (x + 1) * per) of the m-major order, so its workgroups share x rows
+    const int per = (int)(gridDim.x / XCDS);
+    const int tile = (int)(blockIdx.x % XCDS) * per + (int)(blockIdx.x / XCDS);
+    if (tile >= a.tiles) return;
+    const int m0 = (tile / a.nt) * BM;
+    const int n0 = (tile % a.nt) * BN;
 
-    uint4 xv[4];
-    WLoad<BITS> wv;
-    uint32_t sv, bv;
-    auto gload = [&](int g) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) xv[i] = *reinterpret_cast<const uint4 *>(xrow[i] + (size_t)g * BK);
-#pragma unroll
-        for (int p = 0; p < BITS / 4; ++p) wv.v[p] = wbase[(size_t)g * (BITS / 2) + wh * (BITS / 4) + p];
-        sv = srow[g];
-        bv = brow[g];
+    // ---- x tile: thread -> chunk (tid & 7) of rows (tid >> 3) + 64 i, i < 4, 16 B each
+    // (named registers rather than an array, so that they stay out of scratch)
+    const int xr_ = tid >> 3, xc_ = tid & 7;
+    const uint16_t *xs0 = a.x + (size_t)min(m0 + xr_, M - 1) * K + xc_ * 8;
+    const uint16_t *xs1 = a.x + (size_t)min(m0 + xr_ + 64, M - 1) * K + xc_ * 8;
+    const uint16_t *xs2 = a.x + (size_t)min(m0 + xr_ + 128, M - 1) * K + xc_ * 8;
+    const uint16_t *xs3 = a.x + (size_t)min(m0 + xr_ + 192, M - 1) * K + xc_ * 8;
+    const uint32_t xd = swz(xr_, xc_);      // rows + 64 i land at + 64 * 128 * i (same swizzle)
+    uint4 xv0, xv1, xv2, xv3;
+    auto load_x = [&](int g) {
+        const size_t o = (size_t)g * BK;
+        xv0 = *reinterpret_cast<const uint4 *>(xs0 + o);
+        xv1 = *reinterpret_cast<const uint4 *>(xs1 + o);
+        xv2 = *reinterpret_cast<const uint4 *>(xs2 + o);
+        xv3 = *reinterpret_cast<const uint4 *>(xs3 + o);
     };
-    auto lstore = [&](int buf) {
-        uint4 *A = As + buf * TILE_U4;
-        uint4 *B = Bs + buf * TILE_U4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) A[xr[i] * ROW_U4 + xc[i]] = xv[i];
-        const float sf = bf2f(sv), bf = bf2f(bv);
-        uint32_t out[16];
+    auto store_x = [&](int buf) {
+        uint8_t *A = smem + buf * Gm::STAGE + xd;
+        *reinterpret_cast<uint4 *>(A) = xv0;
+        *reinterpret_cast<uint4 *>(A + 64 * ROW_BYTES) = xv1;
+        *reinterpret_cast<uint4 *>(A + 128 * ROW_BYTES) = xv2;
+        *reinterpret_cast<uint4 *>(A + 192 * ROW_BYTES) = xv3;
+    };
+
+    // ---- weights: thread -> (row wr, codes [CPT * wp, CPT * wp + CPT)) of the tile
+    const int wr = tid / Gm::TPR, wp = tid % Gm::TPR;
+    const int wrow = min(n0 + wr, N - 1);
+    const uint8_t *wsrc = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)wrow * ((size_t)K * BITS / 8) +
+                          wp * (CPT * BITS / 8);
+    const uint16_t *ssrc = a.s + (size_t)wrow * G;
+    const uint16_t *bsrc = a.b + (size_t)wrow * G;
+    auto load_w = [&](int g, WRegs<BITS, CPT> &r) {
+        const uint8_t *p = wsrc + (size_t)g * (BK * BITS / 8);
+        if (NW == 4) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(p);
+            r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+        } else if (NW == 8) {
+            const uint4 v0 = *reinterpret_cast<const uint4 *>(p), v1 = *reinterpret_cast<const uint4 *>(p + 16);
+            r.w[0] = v0.x; r.w[1] = v0.y; r.w[2] = v0.z; r.w[3] = v0.w;
+            r.w[4] = v1.x; r.w[5] = v1.y; r.w[6] = v1.z; r.w[7] = v1.w;
+        } else {   // NW == 2
+            const uint2 v = *reinterpret_cast<const uint2 *>(p);
+            r.w[0] = v.x; r.w[1] = v.y;
+        }
+        r.s = ssrc[g];
+        r.b = bsrc[g];
+    };
+    // dequantize quarter qt (CPT / 4 codes) of a thread's codes into weight buffer buf
+    auto store_w = [&](const WRegs<BITS, CPT> &r, int buf, int qt) {
+        uint8_t *B = smem + buf * Gm::STAGE + XTILE;
+        const float sf = bf2f(r.s), bf = bf2f(r.b);
+        constexpr int QC = CPT / 4;                   // codes per quarter: 8 (W4/BN256, W8) or 4
+        uint32_t out[QC / 2];
         if (BITS == 4) {
 #pragma unroll
-            for (int wi = 0; wi < 4; ++wi) {
-                const uint32_t w = wi == 0 ? wv.v[0].x : wi == 1 ? wv.v[0].y : wi == 2 ? wv.v[0].z : wv.v[0].w;
+            for (int h = 0; h < QC / 8; ++h) {
+                const uint32_t w = r.w[qt * (QC / 8) + h];
+                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;   // codes 0,2,4,6 / 1,3,5,7
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float q0 = (float)((w >> (8 * j)) & 0xFu);
-                    const float q1 = (float)((w >> (8 * j + 4)) & 0xFu);
-                    out[wi * 4 + j] = pack_bf16x2(fmaf(sf, q0, bf), fmaf(sf, q1, bf));
-                }
+                for (int j = 0; j < 4; ++j)
+                    out[h * 4 + j] = cvt_pk_bf16(fmaf(sf, ubyte_f32(lo, j), bf), fmaf(sf, ubyte_f32(hi, j), bf));
+            }
+            if (QC == 4) {   // half a word per quarter
+                const uint32_t w = r.w[qt >> 1] >> (16 * (qt & 1));
+                const uint32_t lo = w & 0x0F0Fu, hi = (w >> 4) & 0x0F0Fu;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    out[j] = cvt_pk_bf16(fmaf(sf, ubyte_f32(lo, j), bf), fmaf(sf, ubyte_f32(hi, j), bf));
             }
         } else {
 #pragma unroll
-            for (int wi = 0; wi < 8; ++wi) {
-                const uint4 u = wv.v[wi >> 2];
-                const uint32_t w = (wi & 3) == 0 ? u.x : (wi & 3) == 1 ? u.y : (wi & 3) == 2 ? u.z : u.w;
-                out[wi * 2 + 0] = pack_bf16x2(fmaf(sf, ubyte_f32(w, 0), bf),
-                                              fmaf(sf, ubyte_f32(w, 1), bf));
-                out[wi * 2 + 1] = pack_bf16x2(fmaf(sf, ubyte_f32(w, 2), bf),
-                                              fmaf(sf, ubyte_f32(w, 3), bf));
+            for (int h = 0; h < QC / 4; ++h) {
+                const uint32_t w = r.w[qt * (QC / 4) + h];
+                out[h * 2 + 0] = cvt_pk_bf16(fmaf(sf, ubyte_f32(w, 0), bf), fmaf(sf, ubyte_f32(w, 1), bf));
+                out[h * 2 + 1] = cvt_pk_bf16(fmaf(sf, ubyte_f32(w, 2), bf), fmaf(sf, ubyte_f32(w, 3), bf));
             }
         }
-        uint4 *dst = B + wr * ROW_U4 + wh * 4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = make_uint4(out[4 * i], out[4 * i + 1], out[4 * i + 2], out[4 * i + 3]);
+        // codes [CPT * wp + QC * qt, + QC) are k-chunk (CPT * wp + QC * qt) / 8 of the row
+        const int k0 = CPT * wp + QC * qt;
+        if (QC == 8) {
+            *reinterpret_cast<uint4 *>(B + swz(wr, k0 >> 3)) = make_uint4(out[0], out[1], out[2], out[3]);
+        } else {
+            *reinterpret_cast<uint2 *>(B + swz(wr, k0 >> 3) + ((k0 & 7) ? 8 : 0)) = make_uint2(out[0], out[1]);
+        }
     };
 
-    f32x16_t acc[2][2];
+    f32x16_t acc[4][Gm::NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16_t{};
+        for (int j = 0; j < Gm::NJ; ++j) acc[i][j] = f32x16_t{};
 
-    const int li = lane & 31;
-    const int lh = lane >> 5;
-
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    for (int g = 0; g < G; ++g) {
-        const int buf = g & 1;
-        if (g + 1 < G) gload(g + 1);
-        const uint4 *A = As + buf * TILE_U4;
-        const uint4 *B = Bs + buf * TILE_U4;
+    const int li = lane & 31, lh = lane >> 5;
+    // one stage: MFMAs of stage g (buffer buf) with the dequant of the next stage's
+    // weights (wnext, into buf ^ 1) interleaved a quarter per 16-k step
+    auto stage = [&](int buf, const WRegs<BITS, CPT> &wnext) {
+        const uint8_t *A = smem + buf * Gm::STAGE;
+        const uint8_t *Bt = A + XTILE;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-            bf16x8_t af[2], bfr[2];
+            const int chunk = ks * 2 + lh;
+            bf16x8_t af[4], bfr[Gm::NJ];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = as_bf16x8(A[(wm * 64 + i * 32 + li) * ROW_U4 + ks * 2 + lh]);
+            for (int i = 0; i < 4; ++i)
+                af[i] = as_bf16x8(*reinterpret_cast<const uint4 *>(A + swz(wm * 128 + i * 32 + li, chunk)));
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bfr[j] = as_bf16x8(B[(wn * 64 + j * 32 + li) * ROW_U4 + ks * 2 + lh]);
+            for (int j = 0; j < Gm::NJ; ++j)
+                bfr[j] = as_bf16x8(*reinterpret_cast<const uint4 *>(Bt + swz(wn * Gm::WN + j * 32 + li, chunk)));
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < Gm::NJ; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+            store_w(wnext, buf ^ 1, ks);
         }
-        if (g + 1 < G) lstore(buf ^ 1);
+    };
+
+    // Every load index is clamped to the last stage and every store is unconditional:
+    // past the end they rewrite the buffer not being read, which keeps the loop
+    // free of branches between the MFMAs.
+    const int gl = G - 1;
+    WRegs<BITS, CPT> w0, w1;
+    // prologue: stage 0 in LDS, weights of stage 1 in w1, of stage 2 loading into w0
+    load_w(0, w0);
+    load_x(0);
+    load_w(min(1, gl), w1);
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) store_w(w0, 0, qt);
+    store_x(0);
+    load_w(min(2, gl), w0);
+    __syncthreads();
+    // stage g uses buffer g & 1; w1 holds stage g+1 when g is even, w0 when odd
+    for (int g = 0; g < G; g += 2) {
+        // even stage g: dequant w1 (stage g+1), then load stage g+3 into w1
+        load_x(min(g + 1, gl));
+        stage(0, w1);
+        load_w(min(g + 3, gl), w1);
+        store_x(1);
         __syncthreads();
+        if (g + 1 < G) {   // odd stage g+1: dequant w0 (stage g+2), then load stage g+4 into w0
+            load_x(min(g + 2, gl));
+            stage(1, w0);
+            load_w(min(g + 4, gl), w0);
+            store_x(0);
+            __syncthreads();
+        }
     }
 
-    // epilogue: lane (column j = lane % 32, half h) register r holds row 8*(r/4) + 4h + r%4
+    // ---- epilogue: lane (column li, half lh) register r holds row 8 * (r / 4) + 4 * lh + r % 4
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int j = 0; j < Gm::NJ; ++j) {
+        const int n = n0 + wn * Gm::WN + j * 32 + li;
+        if (n >= N) continue;
+        const float bb = a.bias ? bf2f(a.bias[n]) : 0.f;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int n = n0 + wn * 64 + j * 32 + li;
-            if (n >= N) continue;
-            const float bb = a.bias ? bf2f(a.bias[n]) : 0.f;
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
                 if (m < M) {
                     uint32_t o = f2bf(acc[i][j][r]);
                     if (a.bias) o = f2bf(bf2f(o) + bb);
@@ -179,32 +258,38 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits,
                       hipStream_t stream) {
+    if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "qgemm: bits=%d", bits);
+    if (K % BK) return set_error(SC_EINVAL, "qgemm: K=%d not a multiple of %d", K, BK);
+    if (((uintptr_t)x % 16) || ((uintptr_t)wq % 16))
+        return set_error(SC_EINVAL, "qgemm: x and wq must be 16-byte aligned");
+    // 256-wide tiles when they already give every CU work, else 128-wide
+    const int cus = device_info().num_cus;
+    const int mt = (M + BM - 1) / BM;
+    const bool wide = (long)mt * ((N + 255) / 256) >= cus;
+    const int BNv = wide ? 256 : 128;
+    const int lds = wide ? Geo<256>::LDS : Geo<128>::LDS;
+    if (device_info().max_lds_per_block < lds) return set_error(SC_EUNSUPPORTED, "qgemm: LDS too small");
     GemmArgs a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
     a.M = M; a.N = N; a.K = K; a.G = K / BK;
-    const int lds = 4 * TILE_U4 * 16;
-    dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-    if (bits == 4) {
-        static bool cfg4 = false;
-        if (!cfg4 && lds > 65536) {
-            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(qgemm_mfma_kernel<4>),
+    a.mt = mt;
+    a.nt = (N + BNv - 1) / BNv;
+    a.tiles = a.mt * a.nt;
+    const long blocks = ((long)a.tiles + XCDS - 1) / XCDS * XCDS;
+    if (blocks > 0x7FFFFFFFL) return set_error(SC_EINVAL, "qgemm: grid too large");
+    static bool cfg[2][2] = {};
+    auto go = [&](auto kern, bool &c) -> int {
+        if (!c) {
+            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-            cfg4 = true;
+            c = true;
         }
-        hipLaunchKernelGGL(qgemm_mfma_kernel<4>, grid, dim3(THREADS), lds, stream, a);
-    } else if (bits == 8) {
-        static bool cfg8 = false;
-        if (!cfg8 && lds > 65536) {
-            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(qgemm_mfma_kernel<8>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-            cfg8 = true;
-        }
-        hipLaunchKernelGGL(qgemm_mfma_kernel<8>, grid, dim3(THREADS), lds, stream, a);
-    } else {
-        return set_error(SC_EUNSUPPORTED, "qgemm: bits=%d", bits);
-    }
-    SC_HIP_CHECK(hipGetLastError());
-    return SC_OK;
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(THREADS), lds, stream, a);
+        SC_HIP_CHECK(hipGetLastError());
+        return SC_OK;
+    };
+    if (bits == 4) return wide ? go(qgemm_mfma_kernel<4, 256>, cfg[0][0]) : go(qgemm_mfma_kernel<4, 128>, cfg[0][1]);
+    return wide ? go(qgemm_mfma_kernel<8, 256>, cfg[1][0]) : go(qgemm_mfma_kernel<8, 128>, cfg[1][1]);
 }
 
 }  // namespace sc

@@ -27,6 +27,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return f2bf(lo) | (f2bf(hi) << 16);
 }
 
+// The same rounding (RNE) in one v_cvt_pk_bf16_f32 for finite values; NaN payloads
+// may differ from f2bf, so the bit-compared kernels keep pack_bf16x2.
+typedef __bf16 bf16x2_vt __attribute__((ext_vector_type(2)));
+typedef float f32x2_vt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+    const f32x2_vt v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_vt));
+}
+
 // ---------------------------------------------------------------- exact elementwise math
 //
 // The kernels whose outputs are compared bit for bit (RMSNorm, residual add, SiLU
