@@ -11,7 +11,8 @@ per token.  A "step" is one decode token for the whole batch.
 Printed (one JSON line on stdout):
 * ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
   bracketed by device synchronisation);
-* ``roofline``: the decode qGEMV (``qgemv_dma_kernel<4, 1>``): algorithmic bytes
+* ``roofline``: the decode qGEMV (``qgemv_dma_kernel<4, 1, *, *>``, every
+  prologue/epilogue instantiation: plain, RMSNorm, RMSNorm + SwiGLU): algorithmic bytes
   (packed weights + bf16 scales and biases + x + y) per launch, averaged over the
   129 launches of one decode step, over the average launch duration: HIP events
   on the replay stream around graph replays of exactly those launches (a graph
@@ -21,7 +22,9 @@ Printed (one JSON line on stdout):
 * ``cpu_baseline``: the C restatement of the quantized matmul (OpenMP, fp64
   accumulation) timed on this host on a bounded sample: decoder layer 0's four
   projections plus 1/32 of the lm_head rows at M = batch, repeated for ~10 s,
-  scaled to tokens/s of the 32-layer model's linear layers.
+  scaled to tokens/s of the 32-layer model's linear layers;
+* ``prefill.qgemm_roofline``: the prefill quantized GEMM at M = prompt tokens on
+  layer 0's four projection shapes, TFLOP/s against 2.5 PFLOP/s dense bf16.
 """
 import argparse
 import asyncio
@@ -36,6 +39,7 @@ if ROOT not in sys.path:
 
 METRIC = "W4 decode tok/s (Llama-3-8B shape, bs1) + qGEMV HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK = 2.5e15
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_dma_w4_llama3_8b_decode_traffic.json")
 
 LLAMA3_8B = dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv_heads=8, theta=500000.0, eps=1e-5)
@@ -221,6 +225,48 @@ def time_gemv_launches(model, batch, bits, reps):
                 launches_per_step=len(launches), per_shape=per)
 
 
+def time_prefill_gemms(model, M, bits, reps):
+    """Prefill quantized GEMM (kernel B) per projection shape of layer 0 at M rows:
+    HIP events on the current stream around ``reps`` back-to-back launches (after a
+    warm-up), 2 * M * N * K flops per launch against the 2.5 PFLOP/s dense bf16 peak."""
+    import torch
+    from shardcompute_amd import _lib
+    layer = model.layers[0]
+    att, mlp = layer.attention, layer.mlp
+    K = model.hidden_size
+    shapes = [("qkv", att.qkv._wq, att.qkv._s, att.qkv._b, K, att.qkv.out_features),
+              ("o", att.o_proj.quantized_weight, att.o_proj.scales, att.o_proj.biases_quant,
+               att.o_proj.local_in_features, att.o_proj.out_features),
+              ("gate_up", mlp.gate_up._wq, mlp.gate_up._s, mlp.gate_up._b, K, mlp.gate_up.out_features),
+              ("down", mlp.down_proj.quantized_weight, mlp.down_proj.scales, mlp.down_proj.biases_quant,
+               mlp.down_proj.local_in_features, mlp.down_proj.out_features)]
+    out, tot_fl, tot_us = {}, 0.0, 0.0
+    for name, wq, s, b, k, n in shapes:
+        x = torch.randn((M, k), device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, n), dtype=torch.bfloat16, device="cuda")
+        for _ in range(2):
+            _lib.qmm(x, wq, s, b, bits=bits, path=_lib.PATH_GEMM, out=y)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            _lib.qmm(x, wq, s, b, bits=bits, path=_lib.PATH_GEMM, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        fl = 2.0 * M * n * k
+        tot_fl += fl * len(model.layers)
+        tot_us += us * len(model.layers)
+        out[name] = {"K": k, "N": n, "avg_us": round(us, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 1),
+                     "frac": round(fl / (us * 1e-6) / MFMA_BF16_PEAK, 4)}
+        del x, y
+    agg = tot_fl / (tot_us * 1e-6)
+    log(f"prefill qGEMM at M={M}: " + ", ".join(f"{k} {v['TFLOPs']} TF/s" for k, v in out.items()))
+    return {"kernel": f"qgemm_mfma_kernel<{bits}, *>", "M": M, "bound": "mfma", "unit": "TFLOP/s",
+            "achieved": round(agg / 1e12, 1), "peak": MFMA_BF16_PEAK / 1e12, "frac": round(agg / MFMA_BF16_PEAK, 4),
+            "per_shape": out}
+
+
 def eager_gemv_passes(model, batch, bits, passes):
     """The same launches, eager (for hardware-counter runs, one dispatch at a time)."""
     import torch
@@ -343,6 +389,7 @@ def main():
     first = tokens[0, :8].tolist()
 
     g = time_gemv_launches(model, B, args.bits, args.kernel_reps)
+    gemm = time_prefill_gemms(model, P * B, args.bits, args.kernel_reps) if P * B >= 128 else None
     step_gemv_bytes = g["bytes_per_launch"] * g["launches_per_step"]
     step_gemv_ms = g["avg_us"] * g["launches_per_step"] / 1e3
     traffic = None
@@ -351,7 +398,7 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roof = {"bound": "hbm", "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": f"qgemv_dma_kernel<{args.bits}, 1>" if B == 1 else "qgemv",
+            "kernel": f"qgemv_dma_kernel<{args.bits}, {1 if B == 1 else 8}, *, *>" if B <= 8 else "qgemv",
             "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
             "launches_per_step": g["launches_per_step"]}
 
@@ -375,7 +422,8 @@ def main():
                    "activations": "bf16, fp32 accumulate", "decode": "HIP graph replay per token"},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "prefill": {"tokens": B * P, "ms": round(prefill_s * 1e3, 2), "tok_s": round(B * P / prefill_s, 1)},
+        "prefill": {"tokens": B * P, "ms": round(prefill_s * 1e3, 2), "tok_s": round(B * P / prefill_s, 1),
+                    "qgemm_roofline": gemm},
         "decode_step": {"gemv_ms": round(step_gemv_ms, 4), "gemv_bytes": int(step_gemv_bytes),
                         "kv_bytes_avg": int(kv_bytes),
                         "step_hbm_frac": round((step_gemv_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9
