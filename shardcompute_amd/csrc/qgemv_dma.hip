@@ -25,7 +25,7 @@
 // * Complete tiles are written from registers; a tile split between waves is
 //   summed in wave order from per-wave LDS slots after a barrier, by the wave that
 //   holds its last item (no atomics: results are reproducible run to run).
-#include "sc_common.h"
+#include "dma_util.h"
 
 namespace sc {
 
@@ -65,70 +65,9 @@ struct DmaArgs {
 
 namespace {
 
-constexpr int RING = 3;                     // items per wave ring (RING-1 in flight)
-constexpr int DMA_PER_ITEM = 5;             // 4 weight + 1 scale/bias instruction
-constexpr int SLOT_W = 4096;                // weight bytes per item
-constexpr int SLOT_BYTES = SLOT_W + 1024;   // + scales (lanes 0-15) and biases (16-31)
+using namespace dma;
 constexpr int DMA_MAX_WAVES = 8;
 constexpr int XMAX = 8;                     // input chunks (16 B) per thread in the staging transform
-constexpr int S2_UNITS = SLOT_W / 1024 + 1; // 1 KB staging units in one ring slot
-
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f4;
-
-__device__ __forceinline__ uint32_t wc(uint4 v, int i) { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
-__device__ __forceinline__ uint32_t wh(uint4 v, int i) {
-    const uint32_t w = wc(v, i >> 1);
-    return (i & 1) ? (w >> 16) : (w & 0xFFFFu);
-}
-
-__device__ __forceinline__ uint4 perm_w4x(uint4 v) {
-    uint4 o;
-    o.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
-    o.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
-    o.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
-    o.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
-    return o;
-}
-
-// 16 bytes per active lane from global `g` to LDS byte address lds_base + 16 * lane.
-// The instruction takes its LDS base from M0, which this block sets itself; the
-// kernel has no other M0 user (no LDS-DMA builtins, no indirect register access),
-// so declaring the clobber is all the compiler needs (it warns regardless).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
-                 : "memory", "m0");
-}
-#pragma clang diagnostic pop
-
-// (x & mask) | magic.  VOP3 on gfx950 takes no literal and one scalar operand, so
-// with both constants as literals the compiler emits and + or; with the mask in an
-// SGPR and the magic in a VGPR (both opaque to constant folding) it selects one
-// v_and_or_b32 and still tracks the VALU-write -> MFMA-read hazard itself, which it
-// would not do for the same instruction written as inline asm.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask_sgpr, uint32_t magic_vgpr) {
-    return (x & mask_sgpr) | magic_vgpr;
-}
-
-__device__ __forceinline__ void wait_lgkm0() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Wait until at most n vector-memory operations of this wave are outstanding
-// (lgkmcnt / expcnt untouched).
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(n >= 0 && n < 64, "vmcnt range");
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70 | (n & 15) | ((n >> 4) << 14));
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 
 }  // namespace
 
@@ -585,6 +524,10 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
 
 // ---------------------------------------------------------------- host side
 
+int launch_qgemv_m1(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                    const uint16_t *bias, uint16_t *y, int N, int K, int bits, hipStream_t stream,
+                    const DmaFused *fused);
+
 bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K) {
     (void)x;
     return M >= 1 && M <= 8 && K % 512 == 0 && !((uintptr_t)s % 16) && !((uintptr_t)b % 16) && !((uintptr_t)wq % 16);
@@ -594,6 +537,10 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
                      const DmaFused *fused) {
     if (M < 1 || M > 8) return SC_EUNSUPPORTED;
+    if (M == 1) {       // batch 1: the dynamically balanced kernel (qgemv_m1.hip) when it applies
+        const int rc = launch_qgemv_m1(x, wq, s, b, bias, y, N, K, bits, stream, fused);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
     if (K % 512) return SC_EUNSUPPORTED;                       // 16-byte aligned scale rows, whole items
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16) || ((uintptr_t)wq % 16)) return SC_EUNSUPPORTED;
     const DeviceInfo &di = device_info();

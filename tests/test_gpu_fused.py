@@ -33,7 +33,8 @@ def _bf(rng, shape, scale=1.0):
 
 
 @pytest.mark.parametrize("M,N,K,bits", [(1, 6144, 4096, 4), (3, 1000, 1024, 4), (8, 4096, 2048, 8),
-                                        (1, 520, 576, 4), (16, 512, 1024, 4), (1, 128256, 4096, 4)])
+                                        (1, 520, 576, 4), (16, 512, 1024, 4), (1, 128256, 4096, 4),
+                                        (1, 1000, 512, 4), (1, 1000, 512, 8)])
 def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
     rng = np.random.default_rng(M * 31 + N + K)
     wq, s, b = _weights(rng, N, K, bits)
@@ -62,7 +63,8 @@ def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
 
 @pytest.mark.parametrize("M,I,K,bits,norm", [(1, 14336, 4096, 4, True), (1, 5632, 2048, 4, False),
                                               (3, 1024, 1024, 8, True), (12, 512, 1024, 4, True),
-                                              (1, 2048, 576, 4, True)])
+                                              (1, 2048, 576, 4, True), (1, 256, 512, 4, True),
+                                              (1, 64, 512, 8, False)])
 def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     rng = np.random.default_rng(M * 7 + I + K)
     wq, s, b = _weights(rng, 2 * I, K, bits)
