@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 4
+#define SC_ABI_VERSION 5
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -196,6 +196,28 @@ int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cac
                       int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
                       int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, void *workspace,
                       int64_t workspace_bytes, void *hip_stream);
+
+/* Bytes of workspace sc_attention_decode_bf16 needs (0: none). */
+int64_t sc_attention_decode_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap);
+
+/*
+ * One decode step of attention (one new position per sequence): RoPE of the q and
+ * k heads of qkv row b (rotary position cache_len[0] + pos_offset, tables as for
+ * sc_rope_append_kv_bf16), append of the rotated k and of v at cache slot
+ * cache_len[0], and causal GQA attention of the new position over the cache
+ * (cache_len[0] + 1 keys); out row b at out + b*out_stride.  Equal to
+ * sc_rope_append_kv_bf16 followed by sc_attention_bf16 with S = 1 (same cache
+ * contents afterwards; the output within float rounding, the new key entering the
+ * softmax from registers), with one launch fewer.  H / Hkv <= 16, D 64 or 128.
+ * The qkv row is not modified.  Replaces ParallelAttention.forward's RoPE, KV
+ * concatenation and attention for one token
+ * (src/shardcompute/parallel/attention.py:421-466).
+ */
+int sc_attention_decode_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t H, int64_t Hkv, int64_t D,
+                             const float *cos_t, const float *sin_t, int64_t table_len, uint16_t *k_cache,
+                             uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len, int64_t pos_offset,
+                             float scale, uint16_t *out, int64_t out_stride, void *workspace,
+                             int64_t workspace_bytes, void *hip_stream);
 
 /*
  * out[rows, I] = silu(gate) * up for gate_up [rows, 2I] (gate columns first), with

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -33,6 +33,8 @@ EXPORTS = (
     "sc_rope_append_kv_bf16",
     "sc_attention_workspace_bytes",
     "sc_attention_bf16",
+    "sc_attention_decode_workspace_bytes",
+    "sc_attention_decode_bf16",
     "sc_silu_mul_bf16",
     "sc_argmax_bf16",
     "sc_add_bf16",
@@ -90,6 +92,11 @@ def load():
         lib.sc_attention_workspace_bytes.restype = i64
         lib.sc_attention_bf16.argtypes = [p, i64, p, p, i64, p, p, i64, i64, i64, i64, i64, i64, f32, p, i64, p]
         lib.sc_attention_bf16.restype = i32
+        lib.sc_attention_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64]
+        lib.sc_attention_decode_workspace_bytes.restype = i64
+        lib.sc_attention_decode_bf16.argtypes = [p, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, f32, p,
+                                                 i64, p, i64, p]
+        lib.sc_attention_decode_bf16.restype = i32
         lib.sc_silu_mul_bf16.argtypes = [p, i64, i64, p, p]
         lib.sc_silu_mul_bf16.restype = i32
         lib.sc_argmax_bf16.argtypes = [p, i64, i64, p, p, i64, i64, p, p]
@@ -426,6 +433,41 @@ def attention(q, B, S, H, Hkv, D, k_cache, v_cache_t, cache_len, scale, out=None
                                _ptr(out), out.stride(0), B, S, H, Hkv, D, float(scale), _ptr(workspace), ws_bytes,
                                _stream(q))
     _check(rc, "sc_attention_bf16")
+    return out
+
+
+def attention_decode_workspace_bytes(B, H, Hkv, D, T_cap):
+    return int(load().sc_attention_decode_workspace_bytes(B, H, Hkv, D, T_cap))
+
+
+def attention_decode(qkv, B, H, Hkv, D, cos_t, sin_t, k_cache, v_cache_t, cache_len, scale, pos_offset=0, out=None,
+                     workspace=None):
+    """One decode step of attention: RoPE of row b's q and k heads (rotary position
+    cache_len[0] + pos_offset), append of k and v at slot cache_len[0], and
+    attention of the new position over the cache.  qkv [B, >= (H + 2Hkv) * D] is
+    not modified.  Returns out [B, H*D] bf16."""
+    lib = load()
+    _require_gpu(qkv, cos_t, sin_t, k_cache, v_cache_t, cache_len, out, workspace)
+    _bf16(qkv, "qkv"), _bf16(k_cache, "k_cache"), _bf16(v_cache_t, "v_cache_t"), _i32(cache_len, "cache_len")
+    if qkv.dim() != 2 or qkv.shape[0] != B or qkv.stride(1) != 1:
+        raise ValueError(f"qkv must be a row-major [{B}, *] matrix")
+    T_cap = k_cache.shape[2]
+    if tuple(k_cache.shape) != (B, Hkv, T_cap, D) or tuple(v_cache_t.shape) != (B, Hkv, D, T_cap):
+        raise ValueError("cache shapes must be k [B, Hkv, T_cap, D] and v^T [B, Hkv, D, T_cap]")
+    if (cos_t.dtype != torch.float32 or sin_t.dtype != torch.float32 or cos_t.shape != sin_t.shape
+            or cos_t.dim() != 2 or cos_t.shape[1] != D // 2 or not cos_t.is_contiguous() or not sin_t.is_contiguous()):
+        raise ValueError("cos/sin tables must be contiguous fp32 [L, D/2]")
+    if out is None:
+        out = torch.empty((B, H * D), dtype=torch.bfloat16, device=qkv.device)
+    need = attention_decode_workspace_bytes(B, H, Hkv, D, T_cap)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=qkv.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    rc = lib.sc_attention_decode_bf16(_ptr(qkv), qkv.stride(0), B, H, Hkv, D, _ptr(cos_t), _ptr(sin_t),
+                                      cos_t.shape[0], _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
+                                      int(pos_offset), float(scale), _ptr(out), out.stride(0), _ptr(workspace),
+                                      ws_bytes, _stream(qkv))
+    _check(rc, "sc_attention_decode_bf16")
     return out
 
 

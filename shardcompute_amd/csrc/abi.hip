@@ -38,6 +38,11 @@ int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, l
                        const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
                        long T_cap, const int32_t *cache_len, long pos_offset, hipStream_t stream);
 long attention_workspace_bytes(long B, long S, long H, long Hkv, long D, long T_cap);
+long attention_decode_workspace_bytes(long B, long H, long Hkv, long D, long T_cap);
+int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H, long Hkv, long D,
+                            const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
+                            long T_cap, const int32_t *cache_len, long pos_offset, float scale, uint16_t *out,
+                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream);
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
                      long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream);
@@ -319,6 +324,20 @@ int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cac
                       int64_t workspace_bytes, void *hip_stream) {
     return launch_attention(q, q_stride, k_cache, v_cache_t, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
                             scale, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int64_t sc_attention_decode_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap) {
+    return attention_decode_workspace_bytes(B, H, Hkv, D, T_cap);
+}
+
+int sc_attention_decode_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t H, int64_t Hkv, int64_t D,
+                             const float *cos_t, const float *sin_t, int64_t table_len, uint16_t *k_cache,
+                             uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len, int64_t pos_offset,
+                             float scale, uint16_t *out, int64_t out_stride, void *workspace,
+                             int64_t workspace_bytes, void *hip_stream) {
+    return launch_attention_decode(qkv, qkv_stride, B, H, Hkv, D, cos_t, sin_t, table_len, k_cache, v_cache_t, T_cap,
+                                   cache_len, pos_offset, scale, out, out_stride, workspace, workspace_bytes,
+                                   reinterpret_cast<hipStream_t>(hip_stream));
 }
 
 int sc_silu_mul_bf16(const uint16_t *gate_up, int64_t rows, int64_t I, uint16_t *out, void *hip_stream) {

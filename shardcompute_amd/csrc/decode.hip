@@ -394,6 +394,263 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     for (int e = 0; e < PER; ++e) orow[lane + 64 * e] = (uint16_t)f2bf(acc[e] * inv);
 }
 
+// ---------------------------------------------------------------- decode attention
+//
+// One new position per sequence (S = 1, the decode step): RoPE of q and of the new
+// k, the cache append and attention over the cached keys plus the new one, in one
+// launch (attention.py:421-466 for one token).  Workgroup (key range sp, kv head
+// hk, sequence b), 4 waves:
+// * the first cached-key block's loads are issued before anything else; then q of
+//   the R query heads sharing the kv head is read from the q|k|v row and rotated on
+//   the way in, with rope_append_kernel's arithmetic;
+// * the cached keys [k_lo, min(k_lo + kps, T - 1)) go through attn_block as in
+//   attn_kernel;
+// * the new key and value (position T - 1) never make a round trip through memory
+//   inside the kernel: the range holding T - 1 adds them to wave 0's softmax state
+//   from registers, and writes them into the cache for later steps;
+// * the waves merge in LDS; with one range the result is the output, otherwise the
+//   range's partial goes to the workspace in attn_kernel's layout and
+//   attn_combine_kernel merges the ranges (a cross-XCD merge inside the kernel
+//   costs more than the second launch: coherent stores, a device-scope count and
+//   coherent loads are each a trip to memory).
+struct AttnDecArgs {
+    const uint16_t *qkv;
+    long qkv_stride;         // elements between sequences' rows: q heads, then k, then v
+    const float *cos_t;      // [table_len, D / 2]
+    const float *sin_t;
+    int table_len, pos_offset;
+    uint16_t *kc;            // [B, Hkv, T_cap, D]
+    uint16_t *vt;            // [B, Hkv, D, T_cap]
+    int T_cap;
+    const int32_t *cache_len; // cached positions before this token = its slot
+    uint16_t *out;
+    long out_stride;
+    float *part;             // [B, H, 1, nsplit, D + 4] when nsplit > 1: O[D], m, l, pad
+    int H, Hkv, R, kps, nsplit;
+    float scale_log2;
+};
+
+// dims [i0, i0 + 8) of the first half of a head and their partners i0 + D/2,
+// rotated with the table values (cv, sv) of those dims:
+// bf16(x1 c - x2 s), bf16(x2 c + x1 s)
+__device__ __forceinline__ void rope_pair8(uint4 lo, uint4 hi, const float *cv, const float *sv, uint4 &olo,
+                                           uint4 &ohi) {
+    uint32_t a[4], bb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float r1[2], r2[2];
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = 2 * e + k;
+            const float x1 = bfe(lo, i), x2 = bfe(hi, i);
+            r1[k] = add_rn(mul_rn(x1, cv[i]), mul_rn(-x2, sv[i]));
+            r2[k] = add_rn(mul_rn(x2, cv[i]), mul_rn(x1, sv[i]));
+        }
+        a[e] = pack_bf16x2(r1[0], r1[1]);
+        bb[e] = pack_bf16x2(r2[0], r2[1]);
+    }
+    olo = make_uint4(a[0], a[1], a[2], a[3]);
+    ohi = make_uint4(bb[0], bb[1], bb[2], bb[3]);
+}
+
+template <int D>
+__global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArgs a) {
+    constexpr int U = D / 32;
+    constexpr int DT = D / 16;
+    constexpr int HALF = D / 2;
+    __shared__ float sm_m[ATTN_WAVES][16], sm_l[ATTN_WAVES][16];
+    __shared__ float sm_o[ATTN_WAVES][D][17];
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int sp = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+    const int bh = b * a.Hkv + hk;
+
+    const int pos = a.cache_len[0];                 // slot of the new position
+    const int rpos = pos + a.pos_offset;            // its rotary position
+    // the host sizes cache and tables for every launch; a counter that has run past
+    // them (a stale replay) leaves everything untouched instead of reading or
+    // writing out of bounds
+    if (pos < 0 || pos >= a.T_cap || rpos < 0 || rpos >= a.table_len) return;
+    const int T = pos + 1;                          // keys after the append
+    const int k_lo = sp * a.kps;
+    if (k_lo >= T) return;                          // a range wholly past the keys: the combine never reads it
+    const int k_hi = min(k_lo + a.kps, T - 1);      // cached keys of this range
+    const bool add_new = (T - 1 < k_lo + a.kps) && w == 0;   // wave 0 of the range holding the new position
+
+    // first block of cached keys: issued first, it does not depend on q
+    const uint16_t *kbase = a.kc + (size_t)bh * a.T_cap * D;
+    const uint16_t *vbase = a.vt + (size_t)bh * D * a.T_cap;
+    AttnBlock<D> cur, nxt;
+    const int clampk = a.T_cap - ATTN_KB;
+    int kb = k_lo + ATTN_KB * w;
+    attn_load<D>(cur, kbase, vbase, a.T_cap, min(kb, clampk), c, g);
+
+    // q of head hk * R + c (dims 32u + 8g + [0, 8)), the table row, the new k and v
+    const uint16_t *row = a.qkv + (size_t)b * a.qkv_stride;
+    const bool col_ok = c < a.R;
+    const int limit = col_ok ? T - 2 : -1;          // last cached key a column may see (all of them)
+    uint4 qraw[U], knew[U];
+    uint2 vnew[DT];
+    float cv[U / 2][8], sv[U / 2][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        qraw[u] = make_uint4(0u, 0u, 0u, 0u);
+        knew[u] = make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int n = 0; n < DT; ++n) vnew[n] = make_uint2(0u, 0u);
+    if (col_ok) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            qraw[u] = *reinterpret_cast<const uint4 *>(row + (size_t)(hk * a.R + c) * D + 32 * u + 8 * g);
+    }
+    if (add_new) {
+        const uint16_t *krow = row + (size_t)(a.H + hk) * D;
+        const uint16_t *vrow = row + (size_t)(a.H + a.Hkv + hk) * D;
+#pragma unroll
+        for (int u = 0; u < U; ++u) knew[u] = *reinterpret_cast<const uint4 *>(krow + 32 * u + 8 * g);
+#pragma unroll
+        for (int n = 0; n < DT; ++n) vnew[n] = *reinterpret_cast<const uint2 *>(vrow + 16 * n + 4 * g);
+    }
+    {
+        const float *ct = a.cos_t + (size_t)rpos * HALF, *st = a.sin_t + (size_t)rpos * HALF;
+#pragma unroll
+        for (int u = 0; u < U / 2; ++u) {
+            const float4 c0 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g);
+            const float4 c1 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g + 4);
+            const float4 s0 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g);
+            const float4 s1 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g + 4);
+            cv[u][0] = c0.x; cv[u][1] = c0.y; cv[u][2] = c0.z; cv[u][3] = c0.w;
+            cv[u][4] = c1.x; cv[u][5] = c1.y; cv[u][6] = c1.z; cv[u][7] = c1.w;
+            sv[u][0] = s0.x; sv[u][1] = s0.y; sv[u][2] = s0.z; sv[u][3] = s0.w;
+            sv[u][4] = s1.x; sv[u][5] = s1.y; sv[u][6] = s1.z; sv[u][7] = s1.w;
+        }
+    }
+    bf16x8_t qv[U];
+#pragma unroll
+    for (int u = 0; u < U / 2; ++u) {
+        uint4 lo, hi;
+        rope_pair8(qraw[u], qraw[u + U / 2], cv[u], sv[u], lo, hi);
+        qv[u] = as_bf16x8(lo);
+        qv[u + U / 2] = as_bf16x8(hi);
+    }
+
+    float m = -INFINITY, lsum = 0.f;
+    f4 o[DT];
+#pragma unroll
+    for (int n = 0; n < DT; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // cached keys: the loop of attn_kernel (unconditional, clamped loads)
+    while (true) {
+        const int kn = kb + ATTN_STRIDE;
+        attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
+        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+        if (kn >= k_hi) break;
+        const int kn2 = kn + ATTN_STRIDE;
+        attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
+        attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
+        if (kn2 >= k_hi) break;
+        kb = kn2;
+    }
+
+    // the new key and value: rotate k, append k and v, fold them into wave 0's state
+    if (add_new) {
+        uint4 kr[U];
+#pragma unroll
+        for (int u = 0; u < U / 2; ++u) rope_pair8(knew[u], knew[u + U / 2], cv[u], sv[u], kr[u], kr[u + U / 2]);
+        if (c == 0) {                               // lanes 0, 16, 32, 48 hold every dim once
+            uint16_t *kdst = a.kc + ((size_t)bh * a.T_cap + pos) * D;
+#pragma unroll
+            for (int u = 0; u < U; ++u) *reinterpret_cast<uint4 *>(kdst + 32 * u + 8 * g) = kr[u];
+            uint16_t *vdst = a.vt + (size_t)bh * D * a.T_cap + pos;
+#pragma unroll
+            for (int n = 0; n < DT; ++n) {
+                const int d0 = 16 * n + 4 * g;
+                vdst[(size_t)(d0 + 0) * a.T_cap] = (uint16_t)(vnew[n].x & 0xFFFFu);
+                vdst[(size_t)(d0 + 1) * a.T_cap] = (uint16_t)(vnew[n].x >> 16);
+                vdst[(size_t)(d0 + 2) * a.T_cap] = (uint16_t)(vnew[n].y & 0xFFFFu);
+                vdst[(size_t)(d0 + 3) * a.T_cap] = (uint16_t)(vnew[n].y >> 16);
+            }
+        }
+        // score of the new key for column c: the lane's 8 dims per u, then across g
+        float dot = 0.f;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dot = fmaf(bfe(__builtin_bit_cast(uint4, qv[u]), e), bfe(kr[u], e), dot);
+        dot += __shfl_xor(dot, 16);
+        dot += __shfl_xor(dot, 32);
+        const float sn = col_ok ? dot * a.scale_log2 : -INFINITY;
+        const float mn = fmaxf(m, sn);
+        const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
+        const float p = (sn == -INFINITY) ? 0.f : exp2f(sn - mn);
+        lsum = lsum * alpha + (g == 0 ? p : 0.f);
+        m = mn;
+        const float pb = bf2f(f2bf(p));             // probabilities enter the PV product as bf16
+#pragma unroll
+        for (int n = 0; n < DT; ++n) {
+            const float v4[4] = {__uint_as_float(vnew[n].x << 16), __uint_as_float(vnew[n].x & 0xFFFF0000u),
+                                 __uint_as_float(vnew[n].y << 16), __uint_as_float(vnew[n].y & 0xFFFF0000u)};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[n][r] = fmaf(pb, v4[r], o[n][r] * alpha);
+        }
+    }
+    float ltot = lsum + __shfl_xor(lsum, 16);
+    ltot += __shfl_xor(ltot, 32);
+
+    // ---- merge the 4 waves (as attn_kernel): o[n][r] is O^T[dim 16n + 4g + r][column c]
+    if (g == 0) {
+        sm_m[w][c] = m;
+        sm_l[w][c] = ltot;
+    }
+#pragma unroll
+    for (int n = 0; n < DT; ++n)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sm_o[w][16 * n + 4 * g + r][c] = o[n][r];
+    __syncthreads();
+    const int cc = threadIdx.x & 15;
+    if (cc >= a.R) return;
+    float M = sm_m[0][cc];
+#pragma unroll
+    for (int i = 1; i < ATTN_WAVES; ++i) M = fmaxf(M, sm_m[i][cc]);
+    float wt[ATTN_WAVES], L = 0.f;
+#pragma unroll
+    for (int i = 0; i < ATTN_WAVES; ++i) {
+        wt[i] = (sm_m[i][cc] == -INFINITY) ? 0.f : exp2f(sm_m[i][cc] - M);
+        L += wt[i] * sm_l[i][cc];
+    }
+    constexpr int PER = D * 16 / (64 * ATTN_WAVES);      // dims per thread
+    const int d0 = threadIdx.x >> 4;                     // 0..15
+    const int h = hk * a.R + cc;
+    if (a.nsplit == 1) {
+        const float inv = 1.f / L;
+        uint16_t *orow = a.out + (size_t)b * a.out_stride + (size_t)h * D;
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int d = d0 + 16 * j;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ATTN_WAVES; ++i) acc += wt[i] * sm_o[i][d][cc];
+            orow[d] = (uint16_t)f2bf(acc * inv);
+        }
+    } else {
+        float *pp = a.part + (((size_t)b * a.H + h) * a.nsplit + sp) * (D + 4);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const int d = d0 + 16 * j;
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < ATTN_WAVES; ++i) acc += wt[i] * sm_o[i][d][cc];
+            pp[d] = acc;
+        }
+        if (d0 == 0) {
+            pp[D] = M;
+            pp[D + 1] = L;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- SiLU gate
 //
 // out = (g / (1 + exp(-g))) * u for the fused [rows, 2I] gate|up product
@@ -563,6 +820,65 @@ long attention_workspace_bytes(long B, long S, long H, long Hkv, long D, long T_
     plan_attention(B, S, H, Hkv, D, T_cap, &pl);
     if (pl.a.nsplit == 1) return 0;
     return B * H * S * (long)pl.a.nsplit * (D + 4) * (long)sizeof(float);
+}
+
+long attention_decode_workspace_bytes(long B, long H, long Hkv, long D, long T_cap) {
+    return attention_workspace_bytes(B, 1, H, Hkv, D, T_cap);
+}
+
+int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H, long Hkv, long D,
+                            const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
+                            long T_cap, const int32_t *cache_len, long pos_offset, float scale, uint16_t *out,
+                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream) {
+    if (!qkv || !cos_t || !sin_t || !kc || !vt || !cache_len || !out)
+        return set_error(SC_EINVAL, "attention_decode: null pointer");
+    if (D != 64 && D != 128) return set_error(SC_EUNSUPPORTED, "attention_decode: head_dim %ld (64 or 128 supported)", D);
+    if (B <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || H / Hkv > 16)
+        return set_error(SC_EINVAL, "attention_decode: bad shape B=%ld H=%ld Hkv=%ld (at most 16 q heads per kv head)",
+                         B, H, Hkv);
+    if (B > 65535 || Hkv > 65535) return set_error(SC_EINVAL, "attention_decode: B and Hkv must be below 65536");
+    if (T_cap <= 0 || T_cap % 32 || T_cap >= (1L << 30))
+        return set_error(SC_EINVAL, "attention_decode: cache capacity %ld must be a positive multiple of 32", T_cap);
+    if (table_len <= 0 || table_len >= (1L << 30) || pos_offset < 0 || pos_offset >= (1L << 30))
+        return set_error(SC_EINVAL, "attention_decode: bad rotary table length or offset");
+    if (qkv_stride < (H + 2 * Hkv) * D || out_stride < H * D || qkv_stride % 8 || out_stride % 4)
+        return set_error(SC_EINVAL, "attention_decode: bad row strides");
+    if (((uintptr_t)qkv | (uintptr_t)kc | (uintptr_t)cos_t | (uintptr_t)sin_t) % 16 || ((uintptr_t)vt | (uintptr_t)out) % 8)
+        return set_error(SC_EINVAL, "attention_decode: misaligned pointers");
+    AttnPlan pl;
+    plan_attention(B, 1, H, Hkv, D, T_cap, &pl);
+    AttnArgs ca = pl.a;                                  // the combine's view of the same plan
+    ca.q = nullptr; ca.q_stride = 0; ca.kc = kc; ca.vt = vt; ca.cache_len = cache_len;
+    ca.out = out; ca.out_stride = out_stride;
+    ca.scale_log2 = scale * 1.4426950408889634f;
+    ca.part = nullptr;
+    if (ca.nsplit > 1) {
+        const long need = attention_workspace_bytes(B, 1, H, Hkv, D, T_cap);
+        if (!workspace || workspace_bytes < need)
+            return set_error(SC_EINVAL, "attention_decode: workspace of %ld bytes required", need);
+        if ((uintptr_t)workspace % 16) return set_error(SC_EINVAL, "attention_decode: workspace must be 16-byte aligned");
+        ca.part = static_cast<float *>(workspace);
+    }
+    AttnDecArgs a;
+    a.qkv = qkv; a.qkv_stride = qkv_stride;
+    a.cos_t = cos_t; a.sin_t = sin_t; a.table_len = (int)table_len; a.pos_offset = (int)pos_offset;
+    a.kc = kc; a.vt = vt; a.T_cap = (int)T_cap; a.cache_len = cache_len;
+    a.out = out; a.out_stride = out_stride;
+    a.part = ca.part;
+    a.H = (int)H; a.Hkv = (int)Hkv; a.R = (int)(H / Hkv);
+    a.kps = ca.kps; a.nsplit = ca.nsplit;
+    a.scale_log2 = ca.scale_log2;
+    const dim3 grid((unsigned)a.nsplit, (unsigned)Hkv, (unsigned)B);
+    if (D == 128) hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+    else hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+    SC_HIP_CHECK(hipGetLastError());
+    if (ca.nsplit > 1) {
+        const unsigned cb = (unsigned)((B * H + 3) / 4);
+        if (D == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(cb), dim3(256), 0, stream, ca);
+        else hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(cb), dim3(256), 0, stream, ca);
+        SC_HIP_CHECK(hipGetLastError());
+    }
+    return SC_OK;
 }
 
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,

@@ -76,11 +76,13 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
     const int K = a.K, G = a.G, W = K >> 3;
     const int xunits = K >> 9;                          // 1 KB units of one bf16 row
 
-    // LDS: rings | x (W chunks, permuted for W4) | group sums | per-item partials
+    // LDS: rings | x (W chunks, permuted for W4) | zero block (one item's x chunks) |
+    // group sums | per-item partials
     uint8_t *ring = smem + (size_t)wave * RING * SLOT_BYTES;
     const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
     uint4 *xl = reinterpret_cast<uint4 *>(smem + (size_t)nwaves * RING * SLOT_BYTES);
-    float *xs = reinterpret_cast<float *>(xl + W);
+    uint4 *xzero = xl + W;
+    float *xs = reinterpret_cast<float *>(xzero + 4 * SPAN_WORDS);
     float *part = xs + G;
     // staging: 1 KB unit u lives in ring slot 2 of wave u / S2_UNITS (idle until the
     // ring's first refill, which comes after the staged rows are consumed)
@@ -103,6 +105,7 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
         stage(a.nw, 2);
     }
     if (tid == 0) ctr = 2 * nwaves;                     // items [0, 2 * nwaves) are fixed below
+    if (tid < 4 * SPAN_WORDS) xzero[tid] = make_uint4(0u, 0u, 0u, 0u);
 
     // ---- 2. this workgroup's tiles and the first two items of this wave
     const int P = gridDim.x;
@@ -192,12 +195,15 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
     __syncthreads();
 
     // ---- 4. the ring
-    // A operand: lanes whose A-row carries x (W4: row 0 for the first 16 k of a
-    // 32-k block, row 8 for the second, so D rows 0 and 8 hold the two groups of a
-    // span; W8: row 0), the rest multiply zeros
+    // A operand.  Only D rows 0 and 8 (W4) or row 0 (W8) are used, and row i of D
+    // depends only on row i of A, so every lane loads x for its k-block, except that
+    // W4 uses A-rows 0 and 8 as selectors of the two quantization groups of a span:
+    // row 0 must be zero over the second 16 k of each 32-k block (lanes q = 2, 3) and
+    // row 8 over the first 16 (q = 0, 1).  Those lanes read a zero block.
     const int j = lane & 15, q = lane >> 4;
-    const bool a_on = BITS == 4 ? ((j & 7) == 0 && (j >> 3) == (q >> 1)) : (j == 0);
+    const bool a_zero = BITS == 4 && ((j == 0 && q >= 2) || (j == 8 && q < 2));
     const int epar = BITS == 4 ? (q >> 1) : 0;
+    const int xq = BITS == 4 ? 4 * q : 2 * q;
     // bf16 128.0 in both halves, kept in a VGPR for v_and_or_b32
     uint32_t magic = 0x43004300u;
     asm volatile("" : "+v"(magic));
@@ -214,18 +220,12 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
         const uint4 sv = sl[SLOT_W / 16 + j];
         const uint4 bv = sl[SLOT_W / 16 + 16 + j];
         const int gsub = (ch * ITEM_GROUPS) & 7;        // first group of this item inside the 8 loaded
+        const uint4 *xrow = a_zero ? xzero : xl + ch * 4 * SPAN_WORDS;
         uint4 xa[4][MFMAS];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int u = 0; u < MFMAS; ++u) xa[t][u] = make_uint4(0u, 0u, 0u, 0u);
-        if (a_on) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int u = 0; u < MFMAS; ++u)
-                    xa[t][u] = xl[(ch * 4 + t) * SPAN_WORDS + (BITS == 4 ? 4 * q + u : 2 * q + u)];
-        }
+            for (int u = 0; u < MFMAS; ++u) xa[t][u] = xrow[t * SPAN_WORDS + xq + u];
         float xsv[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) xsv[t] = xs[(ch * 4 + t) * SPAN_GROUPS + epar];
@@ -355,7 +355,8 @@ int launch_qgemv_m1(const uint16_t *x, const uint32_t *wq, const uint16_t *s, co
         P = di.num_cus;
         while (P > 1 && (long)T * CPT < (long)P * w) P /= 2;   // about one item per wave at least
         const long items_max = (long)((T + P - 1) / P) * CPT;
-        lds = (size_t)w * RING * SLOT_BYTES + (size_t)K * 2 + (size_t)G * 4 + (size_t)items_max * 16 * 4;
+        lds = (size_t)w * RING * SLOT_BYTES + (size_t)K * 2 + 4 * 16 * 16 + (size_t)G * 4 +
+              (size_t)items_max * 16 * 4;
         if (lds + static_lds <= (size_t)lds_cap && stage_units <= w * S2_UNITS) {
             waves = w;
             break;

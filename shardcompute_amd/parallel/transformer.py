@@ -160,8 +160,10 @@ class StepBuffers:
         self.gu = torch.empty((rows, 2 * mlp.local_intermediate), dtype=bf, device=dev)
         self.act = torch.empty((rows, mlp.local_intermediate), dtype=bf, device=dev)
         self.hn = torch.empty((B, model.hidden_size), dtype=bf, device=dev)
-        ws = _lib.attention_workspace_bytes(B, S, att.local_num_heads, att.local_num_kv_heads, att.head_dim,
-                                            round_capacity(capacity))
+        H, Hk, D, T_cap = att.local_num_heads, att.local_num_kv_heads, att.head_dim, round_capacity(capacity)
+        ws = _lib.attention_workspace_bytes(B, S, H, Hk, D, T_cap)
+        if S == 1:
+            ws = max(ws, _lib.attention_decode_workspace_bytes(B, H, Hk, D, T_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
 
 

@@ -154,6 +154,116 @@ def test_attention(device, B, S, H, Hkv, D, past, extra):
     assert err <= ATTN_TOL
 
 
+def _decode_case(rng, B, H, Hkv, D, past, T_cap, offset=0, base=500000.0):
+    width = (H + 2 * Hkv) * D + 40                  # row stride wider than the heads
+    rows = _bf(rng, (B, width))
+    k = _bf(rng, (B, Hkv, T_cap, D))                # finite garbage past the cached keys
+    v = _bf(rng, (B, Hkv, T_cap, D))
+    cos_h, sin_h = rope_tables_np(D, base, 1.0, T_cap + offset)
+    return rows, k, v, dev(cos_h), dev(sin_h)
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,past,extra,offset", [
+    (1, 32, 8, 128, 2047, 256, 0),    # Llama-3-8B decode: split keys, merged by the last range
+    (1, 32, 8, 128, 0, 0, 0),         # first position: only the new key
+    (1, 32, 8, 128, 127, 2000, 0),    # the new key opens a range of its own
+    (1, 32, 8, 128, 31, 0, 0),        # the new key at a block boundary
+    (1, 32, 4, 64, 150, 4000, 0),     # TinyLlama heads, mostly empty ranges
+    (16, 32, 8, 128, 300, 0, 0),      # batch 16
+    (4, 8, 1, 128, 1023, 0, 0),       # 70B rank-0 shard heads, batch 4
+    (1, 6, 6, 128, 40, 0, 0),         # no GQA
+    (2, 8, 2, 64, 5, 0, 1000),        # rotary offset (cache-less calls)
+])
+def test_attention_decode_matches_two_kernel_path(device, B, H, Hkv, D, past, extra, offset):
+    rng = np.random.default_rng(B * 11 + H + past + extra)
+    T_cap = ((past + 1 + extra + 31) // 32) * 32
+    rows, k, v, cos_t, sin_t = _decode_case(rng, B, H, Hkv, D, past, T_cap, offset)
+    vt_h = np.ascontiguousarray(v.transpose(0, 1, 3, 2))
+    scale = 1.0 / np.sqrt(D)
+    print(f"attention_decode B={B} H={H} Hkv={Hkv} D={D} past={past} T_cap={T_cap} offset={offset}", flush=True)
+    # fused
+    kc1, vt1 = dev_bf16(k), dev_bf16(vt_h)
+    cnt1 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    qkv1 = dev_bf16(rows)
+    ws = torch.empty(max(_lib.attention_decode_workspace_bytes(B, H, Hkv, D, T_cap), 16), dtype=torch.uint8,
+                     device="cuda")
+    out1 = _lib.attention_decode(qkv1, B, H, Hkv, D, cos_t, sin_t, kc1, vt1, cnt1, scale, pos_offset=offset,
+                                 workspace=ws)
+    # two kernels
+    kc2, vt2 = dev_bf16(k), dev_bf16(vt_h)
+    cnt2 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    qkv2 = dev_bf16(rows)
+    _lib.rope_append_kv(qkv2, B, 1, H, Hkv, D, cos_t, sin_t, kc2, vt2, cnt2, pos_offset=offset)
+    out2 = _lib.attention(qkv2, B, 1, H, Hkv, D, kc2, vt2, cnt2, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vt1, vt2)           # same cache contents
+    assert torch.equal(qkv1, dev_bf16(rows))                        # the q|k|v row is not modified
+    a, b = bf16_to_f32(host_u16(out1)), bf16_to_f32(host_u16(out2))
+    assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max()
+    # against the oracle: rotated q and the cache after the append
+    T = past + 1
+    kh = bf16_to_f32(host_u16(kc1)[:, :, :T])
+    vh = bf16_to_f32(host_u16(vt1)[:, :, :, :T]).transpose(0, 1, 3, 2)
+    cos, sin = rope_cos_sin(np.array([past + offset]), D, 500000.0)
+    q = bf16_to_f32(rows[:, :H * D]).reshape(B, 1, H, D).transpose(0, 2, 1, 3)
+    q = bf16_to_f32(f32_to_bf16(apply_rope(q, cos, sin)))
+    rep = H // Hkv
+    ref = attention_core(q, np.repeat(kh, rep, axis=1), np.repeat(vh, rep, axis=1), scale, T - 1)
+    ref = ref.transpose(0, 2, 1, 3).reshape(B, H * D)
+    assert np.abs(a - ref).max() / np.abs(ref).max() <= ATTN_TOL
+
+
+def test_attention_decode_graph_replays(device):
+    # captured once, replayed with the cache length advancing on the device; every
+    # replay equals the eager two-kernel path at that length
+    B, H, Hkv, D, past, T_cap = 1, 32, 8, 128, 500, 1024
+    rng = np.random.default_rng(77)
+    rows, k, v, cos_t, sin_t = _decode_case(rng, B, H, Hkv, D, past, T_cap)
+    vt_h = np.ascontiguousarray(v.transpose(0, 1, 3, 2))
+    scale = 1.0 / np.sqrt(D)
+    kc1, vt1 = dev_bf16(k), dev_bf16(vt_h)
+    kc2, vt2 = dev_bf16(k), dev_bf16(vt_h)
+    cnt1 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    qkv1 = dev_bf16(rows)
+    ws = torch.empty(max(_lib.attention_decode_workspace_bytes(B, H, Hkv, D, T_cap), 16), dtype=torch.uint8,
+                     device="cuda")
+    out1 = torch.empty((B, H * D), dtype=torch.bfloat16, device="cuda")
+    _lib.attention_decode(qkv1, B, H, Hkv, D, cos_t, sin_t, kc1, vt1, cnt1, scale, out=out1, workspace=ws)
+    _lib.add_i32(cnt1, 1, n=1)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _lib.attention_decode(qkv1, B, H, Hkv, D, cos_t, sin_t, kc1, vt1, cnt1, scale, out=out1, workspace=ws)
+        _lib.add_i32(cnt1, 1, n=1)
+    cnt2 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    for step in range(4):
+        qkv2 = dev_bf16(rows)
+        _lib.rope_append_kv(qkv2, B, 1, H, Hkv, D, cos_t, sin_t, kc2, vt2, cnt2, pos_offset=0)
+        ref = _lib.attention(qkv2, B, 1, H, Hkv, D, kc2, vt2, cnt2, scale)
+        _lib.add_i32(cnt2, 1, n=1)
+        if step > 0:
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = bf16_to_f32(host_u16(out1)), bf16_to_f32(host_u16(ref))
+        assert np.abs(a - b).max() <= 1e-2 * np.abs(b).max(), step
+        assert torch.equal(kc1, kc2) and torch.equal(vt1, vt2), step
+    assert int(cnt1[0]) == past + 4
+
+
+def test_attention_decode_errors(device):
+    qkv = torch.zeros((1, 3 * 256), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 2, 64, 128), dtype=torch.bfloat16, device="cuda")
+    vt = torch.zeros((1, 2, 128, 64), dtype=torch.bfloat16, device="cuda")
+    cnt = torch.zeros(2, dtype=torch.int32, device="cuda")
+    c, s = torch.zeros((64, 64), device="cuda"), torch.zeros((64, 64), device="cuda")
+    with pytest.raises(RuntimeError, match="16 q heads"):
+        _lib.attention_decode(torch.zeros((1, 36 * 128), dtype=torch.bfloat16, device="cuda"), 1, 34, 1, 128, c, s,
+                              torch.zeros((1, 1, 64, 128), dtype=torch.bfloat16, device="cuda"),
+                              torch.zeros((1, 1, 128, 64), dtype=torch.bfloat16, device="cuda"), cnt, 0.1)
+    with pytest.raises(ValueError, match="cos/sin"):
+        _lib.attention_decode(qkv, 1, 2, 2, 128, c[:, :10], s[:, :10], kc, vt, cnt, 0.1)
+
+
 def test_attention_single_key_is_value(device):
     # one cached position: softmax weight 1, output = v exactly (bf16 copy)
     B, S, H, Hkv, D = 1, 1, 8, 2, 128
