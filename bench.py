@@ -11,7 +11,7 @@ per token.  A "step" is one decode token for the whole batch.
 Printed (one JSON line on stdout):
 * ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
   bracketed by device synchronisation);
-* ``roofline``: the decode qGEMV (``qgemv_dma_kernel<4, 1, *, *>``, every
+* ``roofline``: the batch-1 decode qGEMV (``qgemv_m1_kernel<4, *, *>``, every
   prologue/epilogue instantiation: plain, RMSNorm, RMSNorm + SwiGLU): algorithmic bytes
   (packed weights + bf16 scales and biases + x + y) per launch, averaged over the
   129 launches of one decode step, over the average launch duration: HIP events
@@ -40,7 +40,7 @@ if ROOT not in sys.path:
 METRIC = "W4 decode tok/s (Llama-3-8B shape, bs1) + qGEMV HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.5e15
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_dma_w4_llama3_8b_decode_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_m1_w4_llama3_8b_decode_traffic.json")
 
 LLAMA3_8B = dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv_heads=8, theta=500000.0, eps=1e-5)
 
@@ -398,7 +398,8 @@ def main():
             traffic = json.load(f).get("hbm_bytes_per_launch")
     roof = {"bound": "hbm", "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": f"qgemv_dma_kernel<{args.bits}, {1 if B == 1 else 8}, *, *>" if B <= 8 else "qgemv",
+            "kernel": (f"qgemv_m1_kernel<{args.bits}, *, *>" if B == 1 else f"qgemv_dma_kernel<{args.bits}, 8, *, *>")
+                      if B <= 8 else "qgemv",
             "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
             "launches_per_step": g["launches_per_step"]}
 

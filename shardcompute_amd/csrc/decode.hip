@@ -466,66 +466,62 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
     const int sp = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
     const int bh = b * a.Hkv + hk;
 
+    // Loads that do not depend on the cache length go out first, in the order they
+    // are needed (vmcnt retires in order): q, the range's first key block, then
+    // (after the length arrives) the table row and the new key and value.
+    // (Unconditional loads: columns past R read head R - 1 and are masked later; a
+    // conditional load would make the compiler wait for it on the spot.  The length
+    // is read first, as a scalar load that is waited for only where it is used.)
     const int pos = a.cache_len[0];                 // slot of the new position
-    const int rpos = pos + a.pos_offset;            // its rotary position
-    // the host sizes cache and tables for every launch; a counter that has run past
-    // them (a stale replay) leaves everything untouched instead of reading or
-    // writing out of bounds
-    if (pos < 0 || pos >= a.T_cap || rpos < 0 || rpos >= a.table_len) return;
-    const int T = pos + 1;                          // keys after the append
+    const uint16_t *row = a.qkv + (size_t)b * a.qkv_stride;
+    const bool col_ok = c < a.R;
+    uint4 qraw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        qraw[u] = *reinterpret_cast<const uint4 *>(row + (size_t)(hk * a.R + min(c, a.R - 1)) * D + 32 * u + 8 * g);
     const int k_lo = sp * a.kps;
-    if (k_lo >= T) return;                          // a range wholly past the keys: the combine never reads it
-    const int k_hi = min(k_lo + a.kps, T - 1);      // cached keys of this range
-    const bool add_new = (T - 1 < k_lo + a.kps) && w == 0;   // wave 0 of the range holding the new position
-
-    // first block of cached keys: issued first, it does not depend on q
     const uint16_t *kbase = a.kc + (size_t)bh * a.T_cap * D;
     const uint16_t *vbase = a.vt + (size_t)bh * D * a.T_cap;
     AttnBlock<D> cur, nxt;
     const int clampk = a.T_cap - ATTN_KB;
     int kb = k_lo + ATTN_KB * w;
     attn_load<D>(cur, kbase, vbase, a.T_cap, min(kb, clampk), c, g);
+    asm volatile("" ::: "memory");                  // keep these loads ahead of the length check below
 
-    // q of head hk * R + c (dims 32u + 8g + [0, 8)), the table row, the new k and v
-    const uint16_t *row = a.qkv + (size_t)b * a.qkv_stride;
-    const bool col_ok = c < a.R;
+    const int rpos = pos + a.pos_offset;            // its rotary position
+    // the host sizes cache and tables for every launch; a counter that has run past
+    // them (a stale replay) leaves everything untouched instead of reading or
+    // writing out of bounds
+    if (pos < 0 || pos >= a.T_cap || rpos < 0 || rpos >= a.table_len) return;
+    const int T = pos + 1;                          // keys after the append
+    if (k_lo >= T) return;                          // a range wholly past the keys: the combine never reads it
+    const int k_hi = min(k_lo + a.kps, T - 1);      // cached keys of this range
+    const bool has_new = T - 1 < k_lo + a.kps;      // the range holding the new position
+    const bool add_new = has_new && w == 0;         // its wave 0 folds the new key in
     const int limit = col_ok ? T - 2 : -1;          // last cached key a column may see (all of them)
-    uint4 qraw[U], knew[U];
-    uint2 vnew[DT];
+
+    const float *ct = a.cos_t + (size_t)rpos * HALF, *st = a.sin_t + (size_t)rpos * HALF;
     float cv[U / 2][8], sv[U / 2][8];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        qraw[u] = make_uint4(0u, 0u, 0u, 0u);
-        knew[u] = make_uint4(0u, 0u, 0u, 0u);
+    for (int u = 0; u < U / 2; ++u) {
+        const float4 c0 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g);
+        const float4 c1 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g + 4);
+        const float4 s0 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g);
+        const float4 s1 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g + 4);
+        cv[u][0] = c0.x; cv[u][1] = c0.y; cv[u][2] = c0.z; cv[u][3] = c0.w;
+        cv[u][4] = c1.x; cv[u][5] = c1.y; cv[u][6] = c1.z; cv[u][7] = c1.w;
+        sv[u][0] = s0.x; sv[u][1] = s0.y; sv[u][2] = s0.z; sv[u][3] = s0.w;
+        sv[u][4] = s1.x; sv[u][5] = s1.y; sv[u][6] = s1.z; sv[u][7] = s1.w;
     }
-#pragma unroll
-    for (int n = 0; n < DT; ++n) vnew[n] = make_uint2(0u, 0u);
-    if (col_ok) {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            qraw[u] = *reinterpret_cast<const uint4 *>(row + (size_t)(hk * a.R + c) * D + 32 * u + 8 * g);
-    }
-    if (add_new) {
+    uint4 knew[U];                                  // (loaded by every wave: see above)
+    uint2 vnew[DT];
+    {
         const uint16_t *krow = row + (size_t)(a.H + hk) * D;
         const uint16_t *vrow = row + (size_t)(a.H + a.Hkv + hk) * D;
 #pragma unroll
         for (int u = 0; u < U; ++u) knew[u] = *reinterpret_cast<const uint4 *>(krow + 32 * u + 8 * g);
 #pragma unroll
         for (int n = 0; n < DT; ++n) vnew[n] = *reinterpret_cast<const uint2 *>(vrow + 16 * n + 4 * g);
-    }
-    {
-        const float *ct = a.cos_t + (size_t)rpos * HALF, *st = a.sin_t + (size_t)rpos * HALF;
-#pragma unroll
-        for (int u = 0; u < U / 2; ++u) {
-            const float4 c0 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g);
-            const float4 c1 = *reinterpret_cast<const float4 *>(ct + 32 * u + 8 * g + 4);
-            const float4 s0 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g);
-            const float4 s1 = *reinterpret_cast<const float4 *>(st + 32 * u + 8 * g + 4);
-            cv[u][0] = c0.x; cv[u][1] = c0.y; cv[u][2] = c0.z; cv[u][3] = c0.w;
-            cv[u][4] = c1.x; cv[u][5] = c1.y; cv[u][6] = c1.z; cv[u][7] = c1.w;
-            sv[u][0] = s0.x; sv[u][1] = s0.y; sv[u][2] = s0.z; sv[u][3] = s0.w;
-            sv[u][4] = s1.x; sv[u][5] = s1.y; sv[u][6] = s1.z; sv[u][7] = s1.w;
-        }
     }
     bf16x8_t qv[U];
 #pragma unroll
@@ -541,17 +537,23 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
 #pragma unroll
     for (int n = 0; n < DT; ++n) o[n] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // cached keys: the loop of attn_kernel (unconditional, clamped loads)
-    while (true) {
-        const int kn = kb + ATTN_STRIDE;
-        attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
+    // cached keys.  One block per wave (the usual decode split) needs no prefetch: a
+    // useless one would also hold vmcnt slots that the append's stores then wait for.
+    if (kb + ATTN_STRIDE >= k_hi) {
         if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
-        if (kn >= k_hi) break;
-        const int kn2 = kn + ATTN_STRIDE;
-        attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
-        attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
-        if (kn2 >= k_hi) break;
-        kb = kn2;
+    } else {
+        // the loop of attn_kernel (unconditional, clamped loads)
+        while (true) {
+            const int kn = kb + ATTN_STRIDE;
+            attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
+            if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+            if (kn >= k_hi) break;
+            const int kn2 = kn + ATTN_STRIDE;
+            attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
+            attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
+            if (kn2 >= k_hi) break;
+            kb = kn2;
+        }
     }
 
     // the new key and value: rotate k, append k and v, fold them into wave 0's state
@@ -559,19 +561,19 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
         uint4 kr[U];
 #pragma unroll
         for (int u = 0; u < U / 2; ++u) rope_pair8(knew[u], knew[u + U / 2], cv[u], sv[u], kr[u], kr[u + U / 2]);
-        if (c == 0) {                               // lanes 0, 16, 32, 48 hold every dim once
+        // append, one dim (pair) per lane: k dims i and i + D/2, v dims d (the
+        // rotation repeated in this layout, same arithmetic)
+        {
+            const uint16_t *krow = row + (size_t)(a.H + hk) * D;
+            const uint16_t *vrow = row + (size_t)(a.H + a.Hkv + hk) * D;
             uint16_t *kdst = a.kc + ((size_t)bh * a.T_cap + pos) * D;
-#pragma unroll
-            for (int u = 0; u < U; ++u) *reinterpret_cast<uint4 *>(kdst + 32 * u + 8 * g) = kr[u];
             uint16_t *vdst = a.vt + (size_t)bh * D * a.T_cap + pos;
-#pragma unroll
-            for (int n = 0; n < DT; ++n) {
-                const int d0 = 16 * n + 4 * g;
-                vdst[(size_t)(d0 + 0) * a.T_cap] = (uint16_t)(vnew[n].x & 0xFFFFu);
-                vdst[(size_t)(d0 + 1) * a.T_cap] = (uint16_t)(vnew[n].x >> 16);
-                vdst[(size_t)(d0 + 2) * a.T_cap] = (uint16_t)(vnew[n].y & 0xFFFFu);
-                vdst[(size_t)(d0 + 3) * a.T_cap] = (uint16_t)(vnew[n].y >> 16);
+            for (int i = lane; i < HALF; i += 64) {
+                const float x1 = bf2f(krow[i]), x2 = bf2f(krow[i + HALF]);
+                kdst[i] = (uint16_t)f2bf(add_rn(mul_rn(x1, ct[i]), mul_rn(-x2, st[i])));
+                kdst[i + HALF] = (uint16_t)f2bf(add_rn(mul_rn(x2, ct[i]), mul_rn(x1, st[i])));
             }
+            for (int d = lane; d < D; d += 64) vdst[(size_t)d * a.T_cap] = vrow[d];
         }
         // score of the new key for column c: the lane's 8 dims per u, then across g
         float dot = 0.f;
