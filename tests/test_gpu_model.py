@@ -208,3 +208,50 @@ def test_attention_forward_sync_partial(device, weights, model):
     cos, sin = rope_cos_sin(np.arange(7, 12), 64, SHAPE.rope_theta)
     assert np.array_equal(host_u16(q1), f32_to_bf16(apply_rope(bf16_to_f32(host_u16(q)), cos, sin)))
     assert np.array_equal(host_u16(k1), f32_to_bf16(apply_rope(bf16_to_f32(host_u16(k)), cos, sin)))
+
+
+def test_model_loader_roundtrip(device, weights, model, tmp_path):
+    # the same packed weights written as the reference's rank_0/model.safetensors
+    # (Hugging Face names, fp32 scales/biases as the reference's quantizer leaves
+    # them) and loaded through ModelLoader give bit-identical logits
+    from safetensors.torch import save_file
+    from shardcompute_amd.loader import ModelLoader
+
+    def bf(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+    def u32(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).view(torch.uint32)
+
+    W = weights
+    t = {"model.embed_tokens.weight": bf(W["embed"]), "model.norm.weight": bf(W["norm"])}
+    for i, L in enumerate(W["layers"]):
+        p = f"model.layers.{i}"
+        t[f"{p}.input_layernorm.weight"] = bf(L["input_ln"])
+        t[f"{p}.post_attention_layernorm.weight"] = bf(L["post_ln"])
+        for key, name in (("q", "self_attn.q_proj"), ("k", "self_attn.k_proj"), ("v", "self_attn.v_proj"),
+                          ("o", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+                          ("down", "mlp.down_proj")):
+            q = L[key]
+            t[f"{p}.{name}.weight"] = u32(q.wq)
+            t[f"{p}.{name}.scales"] = bf(q.scales).float()
+            t[f"{p}.{name}.biases"] = bf(q.biases).float()
+    lm = W["lm_head"]
+    t["lm_head.weight"], t["lm_head.scales"], t["lm_head.biases"] = u32(lm.wq), bf(lm.scales), bf(lm.biases)
+    (tmp_path / "rank_0").mkdir()
+    save_file(t, str(tmp_path / "rank_0" / "model.safetensors"))
+
+    assert ModelLoader.detect_quantization(tmp_path)
+    m2 = ParallelTransformer(vocab_size=SHAPE.vocab_size, hidden_size=SHAPE.hidden_size,
+                             num_layers=SHAPE.num_layers, num_heads=SHAPE.num_heads,
+                             intermediate_size=SHAPE.intermediate_size, world_size=1, rank=0,
+                             num_kv_heads=SHAPE.num_kv_heads, max_position_embeddings=256,
+                             rms_norm_eps=SHAPE.rms_norm_eps, rope_base=SHAPE.rope_theta, use_quantized=True,
+                             quantization_bits=SHAPE.bits, quantization_group_size=SHAPE.group_size,
+                             embedding="vocab", quantized_lm_head=True)
+    run(ModelLoader(0, 1, quantized=True).load_shards(m2, tmp_path))
+    ids = dev(np.random.default_rng(21).integers(0, SHAPE.vocab_size, (2, 9)).astype(np.int64))
+    a, _ = run(model.forward(ids))
+    b, _ = run(m2.forward(ids))
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
