@@ -257,9 +257,21 @@ def time_prefill_gemms(model, M, bits, reps):
         fl = 2.0 * M * n * k
         tot_fl += fl * len(model.layers)
         tot_us += us * len(model.layers)
+        # context: a dense bf16 GEMM of the same shape (torch.matmul -> hipBLASLt),
+        # without the dequantization, on the same inputs
+        wd = torch.randn((n, k), device="cuda").to(torch.bfloat16)
+        for _ in range(2):
+            torch.matmul(x, wd.t())
+        e0.record()
+        for _ in range(reps):
+            torch.matmul(x, wd.t())
+        e1.record()
+        torch.cuda.synchronize()
+        us_d = e0.elapsed_time(e1) * 1e3 / reps
         out[name] = {"K": k, "N": n, "avg_us": round(us, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 1),
-                     "frac": round(fl / (us * 1e-6) / MFMA_BF16_PEAK, 4)}
-        del x, y
+                     "frac": round(fl / (us * 1e-6) / MFMA_BF16_PEAK, 4),
+                     "dense_bf16_hipblaslt_TFLOPs": round(fl / (us_d * 1e-6) / 1e12, 1)}
+        del x, y, wd
     agg = tot_fl / (tot_us * 1e-6)
     log(f"prefill qGEMM at M={M}: " + ", ".join(f"{k} {v['TFLOPs']} TF/s" for k, v in out.items()))
     return {"kernel": f"qgemm_mfma_kernel<{bits}, *>", "M": M, "bound": "mfma", "unit": "TFLOP/s",

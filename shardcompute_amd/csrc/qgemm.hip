@@ -8,7 +8,7 @@
 //   128 x BN/4 on v_mfma_f32_32x32x16_bf16 (fp32 accumulators).
 // * K advances one quantization group (64) per stage.  LDS holds two stages of the
 //   x tile and of the dequantized weight tile (rows of 128 bytes, 16-byte chunks
-//   swizzled by row & 7 so the MFMA operand reads spread over the banks).
+//   XOR-swizzled by row so the MFMA operand reads are free of bank conflicts).
 // * Loads run ahead of use: the packed weights, scales and biases two stages
 //   ahead (two register sets, so the stage loop is unrolled by two), the x tile one
 //   stage ahead.  During stage g's MFMAs each thread dequantizes its part of stage
@@ -56,8 +56,13 @@ struct Geo {
     static constexpr int CPT = BK / TPR;                         // codes per thread and stage (32 or 16)
 };
 
-// swizzled byte offset of 16-byte chunk c of tile row r
-__device__ __forceinline__ uint32_t swz(int r, int c) { return (uint32_t)(r * ROW_BYTES + ((c ^ (r & 7)) << 4)); }
+// swizzled byte offset of 16-byte chunk c of tile row r: the MFMA operand reads
+// (16 consecutive rows, one chunk) and the row-wise stores (8 chunks of a row, or
+// 2-4 rows) then fall on distinct 16-byte bank groups whether the LDS serves 8
+// lanes over 32 banks or 16 lanes over 64 banks per cycle
+__device__ __forceinline__ uint32_t swz(int r, int c) {
+    return (uint32_t)(r * ROW_BYTES + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4));
+}
 
 template <int BITS, int CPT>
 struct WRegs {
