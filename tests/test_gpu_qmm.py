@@ -182,3 +182,30 @@ def test_leading_dims_and_errors(device):
         _lib.qmm(xm, dev_u32(wq), dev_bf16(s), dev_bf16(b))
     with pytest.raises((RuntimeError, ValueError)):
         _lib.qmm(dev_bf16(x), dev_u32(wq), dev_bf16(s), dev_bf16(b), bits=4, group_size=32)
+
+
+# (K, N, M, bits): the vocab-parallel lm_head of the world_size=2 rank-0 share
+# (64128 rows, the last positions of 64 sequences), and the Llama-3-70B rank-0
+# shard of world_size=8 (q|k|v 8192 -> 1024 + 2 * 128, o 1024 -> 8192, gate|up
+# 8192 -> 2 * 3584, down 3584 -> 8192) at batch-32 decode and 1024-token prefill
+CONFIG_SHAPES = [(4096, 64128, 64, 4)] + [(K, N, M, bits) for (K, N) in
+                                           [(8192, 1280), (1024, 8192), (8192, 7168), (3584, 8192)]
+                                           for M in (32, 1024) for bits in (4, 8)]
+
+
+@pytest.mark.parametrize("K,N,M,bits", CONFIG_SHAPES)
+def test_config_shard_shapes(device, K, N, M, bits):
+    """Sampled rows against the fp64 oracle, every row against the GEMV kernel."""
+    rng = np.random.default_rng(K + 7 * N + M + bits)
+    _, wq, s, b, _ = _case(rng, 1, K, N, bits, False)
+    x = f32_to_bf16(rng.standard_normal((M, K)).astype(np.float32))
+    print(f"config shape K={K} N={N} M={M} bits={bits}", flush=True)
+    y = _run(x, wq, s, b, None, bits, _lib.PATH_AUTO)
+    rows = np.sort(rng.choice(M, min(M, 16), replace=False))
+    ref = f32_to_bf16(quantized_matmul_f64(x[rows], wq, s, b, 64, bits).astype(np.float32))
+    assert_close(y[rows], ref, _lib.PATH_GEMV if M <= 32 else _lib.PATH_GEMM)
+    if M > 32:
+        W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+        xd = dev_bf16(x)
+        yg = torch.cat([_lib.qmm(xd[r0:r0 + 32], *W, bits=bits, path=_lib.PATH_GEMV) for r0 in range(0, M, 32)])
+        assert max_abs_rel(y, host_u16(yg)) <= LINEAR_TOL
