@@ -251,6 +251,60 @@ int sc_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n, 
  */
 int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream);
 
+/*
+ * One batch-1 decode step of the whole decoder trunk in one persistent launch.
+ *
+ * Replaces the per-token pass through the layer stack at one position,
+ * src/shardcompute/parallel/transformer.py:537-559 (embed_tokens, then per layer
+ * ParallelTransformerBlock.forward :214-254 = RMSNorm, ParallelAttention.forward
+ * attention.py:381-471 with QuantizedColumnParallelLinear q/k/v and
+ * QuantizedRowParallelLinear o_proj, RMSNorm, ParallelMLP.forward mlp.py:228-254),
+ * at world_size 1 or one rank's shard with the all-reduces as identity, every
+ * projection an MLX-affine g64 quantized matmul without linear bias.
+ *
+ * Per layer the caller passes the q|k|v rows stacked into one matrix
+ * [(H + 2 Hkv) * D, hidden], o [hidden, H * D], gate|up stacked [2 I, hidden] (gate
+ * rows first), down [hidden, I], the two norm weights and the layer's cache
+ * (batch 1: keys [Hkv, T_cap, D], values transposed [Hkv, D, T_cap]).
+ * `counters[0]` is the new token's cache slot (read on the device at launch),
+ * `ids[0]` its token id.  After the launch `h_out` holds the residual stream that
+ * the final RMSNorm + lm_head read, and every layer's cache holds the new position.
+ *
+ * sc_decode_plan_create validates the shapes (head_dim 128, at most 4 query heads per
+ * kv head, widths multiples of 512, group size 64), uploads the op list and
+ * allocates the plan's exchange buffers (a few MB); sc_decode_plan_run enqueues the
+ * launch on `hip_stream` (capturable: it allocates nothing and calls no memset).
+ * Launches of one plan must not overlap.  sc_decode_plan_status copies the plan's
+ * status word (0: every launch completed; nonzero: a launch gave up after a bounded
+ * wait, outputs invalid) to the host, synchronously.
+ */
+typedef struct sc_decode_layer {
+    const uint32_t *wq_qkv; const uint16_t *s_qkv, *b_qkv;
+    const uint32_t *wq_o; const uint16_t *s_o, *b_o;
+    const uint32_t *wq_gu; const uint16_t *s_gu, *b_gu;
+    const uint32_t *wq_down; const uint16_t *s_down, *b_down;
+    const uint16_t *ln_in, *ln_post;
+    uint16_t *kc, *vt;
+} sc_decode_layer;
+
+typedef struct sc_decode_model {
+    int num_layers, hidden, intermediate, num_heads, num_kv_heads, head_dim, bits, group_size;
+    float eps, scale;                 /* RMSNorm epsilon; attention scale (1/sqrt(head_dim)) */
+    const uint16_t *embed;            /* bf16 [vocab_local, hidden] */
+    int64_t vocab_start, vocab_local;
+    const float *cos_t, *sin_t;       /* fp32 [table_len, head_dim / 2] */
+    int table_len, pos_offset;
+    int T_cap;                        /* cache capacity (multiple of 32) */
+    const int32_t *counters;
+    const int32_t *ids;
+    uint16_t *h_out;                  /* bf16 [hidden] */
+} sc_decode_model;
+
+int sc_decode_plan_create(const sc_decode_model *model, const sc_decode_layer *layers, void **plan_out);
+int sc_decode_plan_run(void *plan, void *hip_stream);
+int sc_decode_plan_status(void *plan, uint32_t *status);
+void sc_decode_plan_destroy(void *plan);
+
 #ifdef __cplusplus
 }
 #endif

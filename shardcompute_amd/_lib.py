@@ -39,6 +39,10 @@ EXPORTS = (
     "sc_argmax_bf16",
     "sc_add_bf16",
     "sc_add_i32",
+    "sc_decode_plan_create",
+    "sc_decode_plan_run",
+    "sc_decode_plan_status",
+    "sc_decode_plan_destroy",
 )
 
 _lib = None
@@ -105,6 +109,14 @@ def load():
         lib.sc_add_bf16.restype = i32
         lib.sc_add_i32.argtypes = [p, i64, i32, p]
         lib.sc_add_i32.restype = i32
+        lib.sc_decode_plan_create.argtypes = [p, p, p]
+        lib.sc_decode_plan_create.restype = i32
+        lib.sc_decode_plan_run.argtypes = [p, p]
+        lib.sc_decode_plan_run.restype = i32
+        lib.sc_decode_plan_status.argtypes = [p, p]
+        lib.sc_decode_plan_status.restype = i32
+        lib.sc_decode_plan_destroy.argtypes = [p]
+        lib.sc_decode_plan_destroy.restype = None
         v = lib.sc_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"libshardcompute_hip ABI {v}, expected {ABI_VERSION}")

@@ -51,6 +51,10 @@ int launch_argmax(const uint16_t *logits, long rows, long V, int32_t *ids, int32
                   long tok_cols, const int32_t *step, hipStream_t stream);
 int launch_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, long n, hipStream_t stream);
 int launch_add_i32(int32_t *p, long n, int32_t delta, hipStream_t stream);
+int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, void **out);
+int decode_plan_run(void *plan, hipStream_t stream);
+int decode_plan_status(void *plan, unsigned *status);
+void decode_plan_destroy(void *plan);
 
 constexpr int PRO_NORM_KIND = 1;
 
@@ -357,6 +361,18 @@ int sc_add_bf16(const uint16_t *a, const uint16_t *b, uint16_t *out, int64_t n, 
 int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream) {
     return launch_add_i32(counters, n, delta, reinterpret_cast<hipStream_t>(hip_stream));
 }
+
+int sc_decode_plan_create(const sc_decode_model *model, const sc_decode_layer *layers, void **plan_out) {
+    return decode_plan_create(model, layers, plan_out);
+}
+
+int sc_decode_plan_run(void *plan, void *hip_stream) {
+    return decode_plan_run(plan, reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_decode_plan_status(void *plan, uint32_t *status) { return decode_plan_status(plan, status); }
+
+void sc_decode_plan_destroy(void *plan) { decode_plan_destroy(plan); }
 
 int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,
                         uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,

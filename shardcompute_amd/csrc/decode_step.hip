@@ -1,0 +1,1198 @@
+// The whole transformer trunk of one batch-1 decode step in one persistent launch.
+//
+// One step of ParallelTransformer.forward at one token (parallel/transformer.py:516-559:
+// embedding, then per layer RMSNorm -> q|k|v -> RoPE + KV append + attention ->
+// o_proj (+ residual) -> RMSNorm -> gate|up -> SiLU gate -> down_proj (+ residual)),
+// with every projection a W4/W8 g64 mx.quantized_matmul (quantized_linear.py:168-176).
+//
+// Why one launch: at batch 1 every projection is a short weight stream (9-66 MB), and
+// as separate launches each pays a launch boundary, a ramp and a tail in which HBM
+// idles.  Here each workgroup (one per CU) streams its share of every op's weights
+// (and of the attention's cached keys and values) through per-wave LDS rings without
+// waiting for the data the op consumes; only the arithmetic waits.  A CU's weight
+// stream for the coming ops keeps running while the step's critical path (norm ->
+// products -> attention -> ...) moves from op to op.
+//
+// Roles inside a workgroup: 8 worker waves claim 4 KB items (16 weight rows x 256 B
+// plus scales/biases, or 8 cached keys with their values) from one counter spanning
+// all ops of the step, DMA them into their ring and compute them; one control wave
+// polls each op's input and publishes each op's output.  At each op boundary all
+// nine waves meet (LDS barriers only) and share the staging work (norm, operand
+// permutation, merging the workers' attention states).  Workgroups exchange activations through "LL" words: 8-byte (data, epoch)
+// pairs written with one agent-coherent store, so a reader that sees the epoch of
+// the current op and launch also sees the data (no flags, no fences, no grid
+// barrier).  Each op kind has its own exchange buffer; a buffer is rewritten one
+// layer later, after every reader has passed an op that needs all workgroups'
+// outputs, so no reader can see a newer write.  Every op's input is the previous
+// op's output.  Epochs are unique per (launch, op).
+//
+// Arithmetic: the projections use the item format, MFMA math and chunk-order
+// partial sums of qgemv_m1_kernel, the norm the 256-thread partition of
+// add_rms_norm_kernel and the rotation rope_append_kernel's, so those results are
+// bit-identical to the per-op path.  Attention (fp32 scores, softmax and
+// probabilities times bf16 values) differs from attn_decode_kernel in rounding only.
+//
+// Every wait is bounded: on a timeout a workgroup sets the status word, skips the
+// remaining work (its waves still pass every op boundary together), drains its DMA
+// and ends.
+#include <algorithm>
+#include <memory>
+#include <vector>
+
+#include "dma_util.h"
+#include "../../include/shardcompute_hip.h"
+
+namespace sc {
+
+namespace step {
+
+using namespace dma;
+
+constexpr int WORKERS = 8;
+constexpr int CTL = WORKERS;                // the control wave
+constexpr int THREADS = 64 * (WORKERS + 1);
+constexpr int SLOT = 4096 + 512;            // item bytes + 16 rows x 8 groups of scales and biases
+#ifndef SC_TRUNK_RING
+#define SC_TRUNK_RING 3
+#endif
+constexpr int TRING = SC_TRUNK_RING;        // ring slots per worker wave (TRING - 1 items in flight)
+constexpr unsigned long long TIMEOUT_TICKS = 20000000ull;   // 200 ms of the 100 MHz real-time clock
+constexpr int HD = 128;                     // head_dim
+constexpr int RMAX = 4;                     // query heads per kv head
+
+constexpr int NT = 6;                       // ops per layer, in this order:
+enum OpKind { K_QKV = 0, K_ATTN = 1, K_MERGE = 2, K_O = 3, K_GU = 4, K_DOWN = 5 };
+enum OpFlags { F_NORM = 1, F_SWIGLU = 2, F_RESID = 4 };
+enum Buf { B_H = 0, B_QKV, B_PART, B_ATT, B_HMID, B_ACT, B_COUNT };
+
+// Shape of one of the four projections of a layer (the same in every layer).
+struct GemvDesc {
+    int N, K, G, T, cpt;
+    unsigned cpt_magic;     // ceil(2^32 / cpt): item / cpt == umulhi(item, cpt_magic)
+    int half;               // F_SWIGLU: output width (gate rows)
+    int flags, in_buf, out_buf;
+};
+
+// Device pointers of one layer: projections q|k|v, o, gate|up, down; norms; cache.
+struct LayerPtrs {
+    const uint32_t *wq[4];
+    const uint16_t *s[4];
+    const uint16_t *b[4];
+    const uint16_t *ln[2];  // input_layernorm, post_attention_layernorm
+    uint16_t *kc, *vt;      // [Hkv, T_cap, D], [Hkv, D, T_cap]
+};
+
+struct Args {
+    const LayerPtrs *layers;  // [L]
+    GemvDesc gd[4];           // q|k|v, o, gate|up, down
+    uint2 *buf[B_COUNT];
+    const int32_t *counters;  // [0]: cached positions before this token (its slot)
+    uint32_t *epoch_base;     // incremented by workgroup 0 at its end
+    unsigned *status;         // 0 ok; nonzero: a launch gave up
+    const int32_t *ids;       // the step's token id
+    const uint16_t *embed;    // [V_local, hidden]
+    const float *cos_t, *sin_t;
+    uint16_t *h_out;          // the last layer's output (plain bf16)
+    long vocab_start;
+    int V_local, table_len, pos_offset;
+    int L, nops, hidden, H, Hkv, R, NR, T_cap, C_merge;
+    float eps, scale_log2;
+    // LDS layout (byte offsets into dynamic shared memory)
+    int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
+};
+
+__device__ __forceinline__ void ll_store(uint2 *p, uint32_t data, uint32_t ep) {
+    const unsigned long long v = (unsigned long long)data | ((unsigned long long)ep << 32);
+    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long ll_load(const uint2 *p) {
+    return __hip_atomic_load(reinterpret_cast<const unsigned long long *>(p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ unsigned long long now() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Tiles [tb, te) of a projection with T tiles owned by workgroup wg of P.
+__device__ __forceinline__ void gemv_tiles(int T, int wg, int P, int &tb, int &te) {
+    tb = (int)((unsigned)wg * (unsigned)T / (unsigned)P);
+    te = (int)((unsigned)(wg + 1) * (unsigned)T / (unsigned)P);
+}
+
+__device__ __forceinline__ int gemv_index(int kind) {
+    return kind == K_QKV ? 0 : kind == K_O ? 1 : kind == K_GU ? 2 : 3;
+}
+
+// Lane reductions on the VALU: DPP moves within rows of 16 lanes and the permlane
+// swaps across rows, no LDS round trip.  Each step adds (or maxes) two operands, so
+// every lane of a group ends with the same bits.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1;          // quad_perm [1, 0, 3, 2]
+constexpr int DPP_XOR2 = 0x4E;          // quad_perm [2, 3, 0, 1]
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane i of 8 <- lane 7 - i
+constexpr int DPP_ROR8 = 0x128;         // lane i of 16 <- lane (i + 8) mod 16
+// (rows 0 1 2 3) -> a = (r0 r0 r2 r2), b = (r1 r1 r3 r3)
+__device__ __forceinline__ void swap16(float v, float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+// (lanes 0-31, 32-63) -> a = (lo lo), b = (hi hi)
+__device__ __forceinline__ void swap32(float v, float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+// sum over the 8 lanes 8g .. 8g + 7
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_mov<DPP_XOR1>(v);
+    v += dpp_mov<DPP_XOR2>(v);
+    return v + dpp_mov<DPP_HALF_MIRROR>(v);
+}
+// v equal within each group of 8 lanes: sum / max over the 8 groups
+__device__ __forceinline__ float groups_sum(float v) {
+    float a, b;
+    v += dpp_mov<DPP_ROR8>(v);
+    swap16(v, a, b);
+    swap32(a + b, a, b);
+    return a + b;
+}
+__device__ __forceinline__ float groups_max(float v) {
+    float a, b;
+    v = fmaxf(v, dpp_mov<DPP_ROR8>(v));
+    swap16(v, a, b);
+    swap32(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float lanes_sum(float v) { return groups_sum(group8_sum(v)); }
+__device__ __forceinline__ float lanes_max(float v) {
+    v = fmaxf(v, dpp_mov<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_mov<DPP_XOR2>(v));
+    return groups_max(fmaxf(v, dpp_mov<DPP_HALF_MIRROR>(v)));
+}
+
+struct AttnUnit {
+    int valid, kvh, r, lo, hi;   // keys [lo, hi) of kv head kvh (hi includes the new position)
+};
+
+__device__ __forceinline__ AttnUnit attn_unit(const Args &a, int wg, int T, int kps) {
+    AttnUnit u;
+    u.valid = wg < a.Hkv * a.NR;
+    u.kvh = u.valid ? wg / a.NR : 0;
+    u.r = u.valid ? wg - u.kvh * a.NR : 0;
+    u.lo = u.r * kps;
+    u.hi = min(u.lo + kps, T);
+    return u;
+}
+
+}  // namespace step
+
+using namespace step;
+
+template <int BITS>
+__global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
+    constexpr int SPAN_K = BITS == 4 ? 128 : 64;
+    constexpr int SPAN_GROUPS = SPAN_K / 64;
+    constexpr int SPAN_WORDS = SPAN_K / 8;
+    constexpr int ITEM_K = 4 * SPAN_K;
+    constexpr int ITEM_GROUPS = ITEM_K / 64;
+    constexpr int MFMAS = BITS == 4 ? 4 : 2;
+    constexpr int D = HD;
+    constexpr int AST = RMAX * (D + 2);     // floats per attention item state
+
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ int s_ctr;                   // next stream item to claim
+    __shared__ int s_pre[NT + 1];           // this workgroup's items per layer, prefix over op kinds
+    __shared__ int s_total;
+    __shared__ int s_abort;                 // a poll gave up: every wave skips the remaining work
+    __shared__ float s_red[NORM_THREADS / 64];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int P = gridDim.x, wg = blockIdx.x;
+    const int nops = a.nops;
+
+    uint4 *xl = reinterpret_cast<uint4 *>(smem + a.o_xl);
+    uint4 *xzero = reinterpret_cast<uint4 *>(smem + a.o_xzero);
+    float *xs = reinterpret_cast<float *>(smem + a.o_xs);
+    float *part = reinterpret_cast<float *>(smem + a.o_part);
+    uint4 *hbuf = reinterpret_cast<uint4 *>(smem + a.o_hbuf);
+    uint16_t *qkv_l = reinterpret_cast<uint16_t *>(smem + a.o_qkv);   // q [RMAX][D], k [D], v [D] (bf16)
+    GemvDesc *sgd = reinterpret_cast<GemvDesc *>(smem + a.o_gd);
+    LayerPtrs *slp = reinterpret_cast<LayerPtrs *>(smem + a.o_lp);
+    float *ast = reinterpret_cast<float *>(smem + a.o_xl);              // attention states (overlay x)
+
+    const int pos = a.counters[0];
+    const int T = pos + 1;                  // keys after the append
+    int kps = (T + a.NR - 1) / a.NR;
+    kps = (kps + 7) & ~7;
+    const uint32_t base = a.epoch_base[0];
+    const AttnUnit au = attn_unit(a, wg, T, kps);
+
+    // ---- set-up by the control wave: shapes and layer pointers into LDS, this
+    // workgroup's items per op kind; then the one workgroup-wide barrier
+    if (wave == WORKERS) {
+        {
+            const uint4 *src = reinterpret_cast<const uint4 *>(a.layers);
+            uint4 *dst = reinterpret_cast<uint4 *>(slp);
+            const int n = a.L * (int)(sizeof(LayerPtrs) / 16);
+            for (int c = lane; c < n; c += 64) dst[c] = src[c];
+        }
+        if (lane < 4) {
+            const GemvDesc g = lane == 0 ? a.gd[0] : lane == 1 ? a.gd[1] : lane == 2 ? a.gd[2] : a.gd[3];
+            sgd[lane] = g;
+        }
+        if (lane == 0) {
+            // a cache slot outside the cache or the rotary table (a stale replay): the
+            // workers get no items (no DMA is issued) and the launch ends at once
+            const bool valid = pos >= 0 && pos < a.T_cap && pos + a.pos_offset < a.table_len;
+            int acc = 0;
+            for (int k = 0; k < NT; ++k) {
+                s_pre[k] = acc;
+                int n = 0;
+                if (k == K_ATTN) {
+                    if (au.valid && au.lo < au.hi) n = (au.hi - au.lo + 7) >> 3;
+                } else if (k != K_MERGE) {
+                    const int gi = gemv_index(k);
+                    const GemvDesc g = gi == 0 ? a.gd[0] : gi == 1 ? a.gd[1] : gi == 2 ? a.gd[2] : a.gd[3];
+                    int tb, te;
+                    gemv_tiles(g.T, wg, P, tb, te);
+                    n = (te - tb) * g.cpt;
+                }
+                acc += n;
+            }
+            s_pre[NT] = acc;
+            s_total = valid ? acc * a.L : 0;
+            s_ctr = (TRING - 1) * WORKERS;
+            s_abort = valid ? 0 : 1;
+            if (!valid) __hip_atomic_store(a.status, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        for (int c = lane; c < 4 * SPAN_WORDS; c += 64) xzero[c] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    __syncthreads();
+
+    // ====================================================================== op boundaries
+    //
+    // Every wave calls boundary(jj) for jj = 0 .. nops in order, exactly once each
+    // (workers as soon as their next item belongs to op jj or later, so all their
+    // items of op jj - 1 are computed).  boundary(jj) finishes op jj - 1 (reduces its
+    // partials and publishes its output) and stages op jj's input in LDS.  The control
+    // wave publishes, polls narrow inputs and appends to the cache; every wave polls
+    // wide inputs.  __syncthreads waits on LDS only.
+    const bool ctl = wave == CTL;
+    const unsigned long long t_start = now();
+    auto timed_out = [&]() -> bool {
+        if (now() - t_start > TIMEOUT_TICKS) {
+            __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            return true;
+        }
+        return false;
+    };
+
+    // Control wave: gather n8 chunks of 8 bf16 (chunk c = LL words [addr(c), +4)) that
+    // carry epoch ep; put(c, v) receives each chunk once (per lane; no cross-lane
+    // operations inside).  Batches of 4 chunks per lane; the first pass keeps two
+    // batches in flight (one round trip for inputs that are already published), later
+    // passes re-read the batches still missing a chunk.
+    auto ll_gather = [&](auto addr, int n8, uint32_t ep, auto put) __attribute__((always_inline)) -> bool {
+        constexpr int CPL = 4;                           // chunks per lane per batch
+        constexpr int BCH = 64 * CPL;                    // chunks per batch
+        const int nb = (n8 + BCH - 1) / BCH;             // at most 8 (host: widths <= 16384)
+        uint32_t pend = 0u;                              // bit CPL bi + i: chunk bi * BCH + 64 i + lane missing
+        for (int bi = 0; bi < nb; ++bi)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i)
+                if (bi * BCH + i * 64 + lane < n8) pend |= 1u << (CPL * bi + i);
+        auto load = [&](int bi, unsigned long long (&v)[4 * CPL]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                const uint2 *p = addr(min(bi * BCH + i * 64 + lane, n8 - 1));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[4 * i + k] = ll_load(p + k);
+            }
+        };
+        auto check = [&](int bi, const unsigned long long (&v)[4 * CPL]) __attribute__((always_inline)) {
+            const uint32_t pb = (pend >> (CPL * bi)) & ((1u << CPL) - 1u);
+#pragma unroll
+            for (int i = 0; i < CPL; ++i) {
+                if (pb & (1u << i)) {
+                    bool okc = true;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) okc = okc && (uint32_t)(v[4 * i + k] >> 32) == ep;
+                    if (okc) {
+                        put(bi * BCH + i * 64 + lane, make_uint4((uint32_t)v[4 * i], (uint32_t)v[4 * i + 1],
+                                                               (uint32_t)v[4 * i + 2], (uint32_t)v[4 * i + 3]));
+                        pend &= ~(1u << (CPL * bi + i));
+                    }
+                }
+            }
+        };
+        unsigned long long va[4 * CPL], vb[4 * CPL];
+        load(0, va);
+        for (int bi = 0; bi < nb; bi += 2) {
+            if (bi + 1 < nb) load(bi + 1, vb);
+            check(bi, va);
+            if (bi + 2 < nb) load(bi + 2, va);
+            if (bi + 1 < nb) check(bi + 1, vb);
+        }
+        for (int it = 0; __ballot(pend != 0u) != 0ull; ++it) {
+            for (int bi = 0; bi < nb; ++bi) {
+                if (__ballot(((pend >> (CPL * bi)) & ((1u << CPL) - 1u)) != 0u) == 0ull) continue;
+                load(bi, va);
+                check(bi, va);
+            }
+            if ((it & 15) == 15 && (timed_out() ||
+                __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
+                return false;
+        }
+        return true;
+    };
+
+    // Every wave: gather the raw chunks of a wide input (chunk c = LL words [4c, 4c + 4) of
+    // src) into x, the blocks of 64 chunks dealt round-robin to the nine waves (at most 4
+    // per wave).  Chunks that are not all there are then watched through their last word
+    // only, with a short sleep between polls, and re-read once it carries the epoch: 2304
+    // waves re-reading whole inputs would flood L2 ahead of the producers' weight reads.
+    // A worker's waits here also cover its older weight DMA (vmcnt retires in order).
+    auto gather_all = [&](const uint2 *src, int n8, uint32_t ep) __attribute__((always_inline)) -> bool {
+        constexpr int NW = WORKERS + 1;
+        uint32_t pend = 0u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if ((wave + NW * i) * 64 + lane < n8) pend |= 1u << i;
+        uint32_t fetch = pend;                          // chunks to read whole this round
+        const uint2 *wsrc = src + 4 * 64 * wave;        // wave-uniform base + lane offset
+        const uint32_t lane_w = 4u * lane;
+        for (int it = 0;; ++it) {
+            unsigned long long v[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint2 *p = wsrc + 4 * 64 * NW * i + lane_w;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) v[4 * i + k] = (fetch & (1u << i)) ? ll_load(p + k) : 0ull;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (fetch & (1u << i)) {
+                    bool okc = true;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) okc = okc && (uint32_t)(v[4 * i + k] >> 32) == ep;
+                    if (okc) {
+                        xl[(wave + NW * i) * 64 + lane] = make_uint4((uint32_t)v[4 * i], (uint32_t)v[4 * i + 1],
+                                                                    (uint32_t)v[4 * i + 2], (uint32_t)v[4 * i + 3]);
+                        pend &= ~(1u << i);
+                    }
+                }
+            }
+            if (__ballot(pend != 0u) == 0ull) return true;
+            fetch = 0u;
+            for (int sp = 0;; ++sp) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (pend & (1u << i)) {
+                        const uint2 *p = wsrc + 4 * 64 * NW * i + lane_w;
+                        if ((uint32_t)(ll_load(p + 3) >> 32) == ep) fetch |= 1u << i;
+                    }
+                }
+                if (__ballot(fetch != 0u) != 0ull) break;
+                __builtin_amdgcn_s_sleep(2);
+                if ((sp & 15) == 15 && (timed_out() ||
+                    __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
+                    return false;
+            }
+            if ((it & 15) == 15 && (timed_out() ||
+                __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
+                return false;
+        }
+    };
+
+    // x chunk c of a projection input into LDS: W4 operand permutation + 64-element
+    // group sums (the 8 chunks of a group in 8 adjacent lanes); lanes converged
+    auto put_x = [&](int c, uint4 v) {
+        xl[c] = BITS == 4 ? perm_w4x(v) : v;
+        float g = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) g += bfe(v, e);
+        g += __shfl_xor(g, 1);
+        g += __shfl_xor(g, 2);
+        g += __shfl_xor(g, 4);
+        if ((c & 7) == 0) xs[c >> 3] = g;
+    };
+
+    auto epoch = [&](int j) -> uint32_t { return base * (uint32_t)nops + (uint32_t)j + 1u; };
+    auto kind_of = [&](int j) -> int { return j == 0 ? -1 : (j - 1) % NT; };
+
+    auto boundary = [&](int jj) __attribute__((always_inline)) {
+        __syncthreads();                                             // B1: op jj - 1 computed
+        const int jp = jj - 1;
+        // ------------------------------------------------------------ finish op jp
+        if (jp >= 0 && !s_abort) {
+            const int kp = kind_of(jp);
+            const int lp_ = jp == 0 ? -1 : (jp - 1) / NT;
+            const uint32_t ep = epoch(jp);
+            if (kp == K_ATTN) {
+                if (au.valid) {
+                    // merge the items' (m, l, O) per head, in item order (the same sums
+                    // whichever wave computed which item), into part: [R][D + 2] = O
+                    // (unnormalised), m, l
+                    const int ni = au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
+                    for (int t = tid; t < a.R * (D + 2); t += THREADS) {
+                        const int h = t / (D + 2), x = t - h * (D + 2);
+                        float M = -INFINITY;
+                        for (int w = 0; w < ni; ++w) M = fmaxf(M, ast[w * AST + h * (D + 2) + D]);
+                        float acc = 0.f;
+                        for (int w = 0; w < ni; ++w) {
+                            const float mw = ast[w * AST + h * (D + 2) + D];
+                            if (mw != -INFINITY) {
+                                const float e = exp2f(mw - M);
+                                if (x == D) acc = M;
+                                else if (x == D + 1) acc = fmaf(e, ast[w * AST + h * (D + 2) + D + 1], acc);
+                                else acc = fmaf(e, ast[w * AST + h * (D + 2) + x], acc);
+                            }
+                        }
+                        part[t] = (x == D) ? M : acc;
+                    }
+                    __syncthreads();
+                    if (ctl) {
+                        uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
+                        for (int t = lane; t < a.R * (D + 2); t += 64) ll_store(dst + t, __float_as_uint(part[t]), ep);
+                    }
+                }
+            } else if (kp != K_MERGE && ctl) {
+                if (jp == 0) {
+                    // this workgroup's words of the hidden row: masked gather (embedding.py:322-356)
+                    const int words = a.hidden / 2;
+                    const int per = (words + P - 1) / P;
+                    const int id = a.ids[0];
+                    const long local = (long)id - a.vocab_start;
+                    const bool inr = local >= 0 && local < a.V_local;
+                    const uint32_t *row =
+                        reinterpret_cast<const uint32_t *>(a.embed + (inr ? local : 0) * (size_t)a.hidden);
+                    for (int w = wg * per + lane; w < min(words, (wg + 1) * per); w += 64)
+                        ll_store(a.buf[B_H] + w, inr ? row[w] : 0u, ep);
+                } else {
+                    const GemvDesc &o = sgd[gemv_index(kp)];
+                    int tb, te;
+                    gemv_tiles(o.T, wg, P, tb, te);
+                    const int ntl = te - tb, cpt = o.cpt;
+                    uint2 *dst = a.buf[o.out_buf];
+                    uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
+                    if (o.flags & F_SWIGLU) {
+                        // tile tl: gate columns 8 (tb + tl) + c, c < 8; 4 words per tile
+                        for (int wdx = lane; wdx < ntl * 4; wdx += 64) {
+                            const int tl = wdx >> 2, c = 2 * (wdx & 3);
+                            const float *pp = part + (size_t)tl * cpt * 16;
+                            float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+                            for (int ch = 0; ch < cpt; ++ch) {
+                                g0 += pp[ch * 16 + c];
+                                g1 += pp[ch * 16 + c + 1];
+                                u0 += pp[ch * 16 + 8 + c];
+                                u1 += pp[ch * 16 + 8 + c + 1];
+                            }
+                            const uint32_t o0 = f2bf(silu_mul_f(bf2f(f2bf(g0)), bf2f(f2bf(u0))));
+                            const uint32_t o1 = f2bf(silu_mul_f(bf2f(f2bf(g1)), bf2f(f2bf(u1))));
+                            ll_store(dst + ((tb + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
+                        }
+                    } else {
+                        const uint32_t *hw = reinterpret_cast<const uint32_t *>(hbuf);
+                        const bool resid = o.flags & F_RESID;
+                        for (int wdx = lane; wdx < ntl * 8; wdx += 64) {
+                            const int tl = wdx >> 3, c = 2 * (wdx & 7);
+                            const float *pp = part + (size_t)tl * cpt * 16;
+                            float v0 = 0.f, v1 = 0.f;
+                            for (int ch = 0; ch < cpt; ++ch) {
+                                v0 += pp[ch * 16 + c];
+                                v1 += pp[ch * 16 + c + 1];
+                            }
+                            const int n = (tb + tl) * 16 + c;
+                            uint32_t o0 = f2bf(v0), o1 = f2bf(v1);
+                            if (resid) {
+                                const uint32_t hv = hw[n / 2];
+                                o0 = f2bf(add_rn(bf2f(hv & 0xFFFFu), bf2f(o0)));
+                                o1 = f2bf(add_rn(bf2f(hv >> 16), bf2f(o1)));
+                            }
+                            ll_store(dst + n / 2, o0 | (o1 << 16), ep);
+                            if (plain) *reinterpret_cast<uint32_t *>(plain + n) = o0 | (o1 << 16);
+                        }
+                    }
+                }
+            }
+        }
+        if (jj >= nops) return;
+        // ------------------------------------------------------------ stage op jj
+        const int k = kind_of(jj);
+        const int l = jj == 0 ? -1 : (jj - 1) / NT;
+        const uint32_t ep_in = epoch(jj - 1);                        // every op reads the previous op's output
+        const bool is_gemv = k == K_QKV || k == K_O || k == K_GU || k == K_DOWN;
+        const GemvDesc &o = sgd[is_gemv ? gemv_index(k) : 0];
+        const int W = o.K >> 3;
+        const bool wide = is_gemv && !(o.flags & F_NORM) && W > 512;     // every wave polls
+        if (wide && !s_abort) {
+            if (!gather_all(a.buf[o.in_buf], W, ep_in) && lane == 0) s_abort = 1;
+        } else if (ctl && !s_abort) {
+            bool ok = true;
+            if (is_gemv) {
+                const uint2 *src = a.buf[o.in_buf];
+                auto addr = [&](int c) -> const uint2 * { return src + 4 * (size_t)c; };
+                if (o.flags & F_NORM) {
+                    // the norm weight lands in x's LDS (chunk c at x[c]) while the input is
+                    // polled; the transform overwrites chunk c only after reading it
+                    const uint8_t *nw = reinterpret_cast<const uint8_t *>(slp[l].ln[k == K_QKV ? 0 : 1]);
+                    const uint32_t xl_lds = (uint32_t)(uintptr_t)xl;
+                    for (int c0 = 0; c0 < W; c0 += 64) dma16(nw + (size_t)(c0 + lane) * 16, xl_lds + c0 * 16);
+                    // raw h into hbuf (kept for the residual epilogue)
+                    ok = ll_gather(addr, W, ep_in, [&](int c, uint4 v) { hbuf[c] = v; });
+                    wait_vm<0>();
+                } else {
+                    ok = ll_gather(addr, W, ep_in, [&](int c, uint4 v) { xl[c] = v; });
+                }
+            } else if (k == K_ATTN) {
+                if (au.valid) {
+                    const int rpos = pos + a.pos_offset;
+                    const float *ct = a.cos_t + (size_t)rpos * (D / 2), *st = a.sin_t + (size_t)rpos * (D / 2);
+                    const float cv = ct[lane], sv = st[lane];     // loads overlap the poll
+                    const uint2 *src = a.buf[B_QKV];
+                    const int qc = a.R * D / 8;                 // q chunks, then k (D / 8), then v (D / 8)
+                    auto addr = [&](int c) -> const uint2 * {
+                        size_t e;
+                        if (c < qc) e = (size_t)(au.kvh * a.R) * D + (size_t)c * 8;
+                        else if (c < qc + D / 8) e = (size_t)(a.H + au.kvh) * D + (size_t)(c - qc) * 8;
+                        else e = (size_t)(a.H + a.Hkv + au.kvh) * D + (size_t)(c - qc - D / 8) * 8;
+                        return src + e / 2;
+                    };
+                    uint4 *raw = reinterpret_cast<uint4 *>(qkv_l);
+                    ok = ll_gather(addr, qc + 2 * (D / 8), ep_in, [&](int c, uint4 v) {
+                        raw[c < qc ? c : RMAX * D / 8 + (c - qc)] = v;      // q heads, then k at RMAX, v after it
+                    });
+                    if (ok) {
+                        // rotate the q heads and the new key in place (rope_append_kernel's
+                        // arithmetic): lane = dim i of the first half, pairs (i, i + D/2)
+                        for (int h = 0; h <= a.R; ++h) {
+                            uint16_t *row = qkv_l + (h < a.R ? h * D : RMAX * D);
+                            const float x1 = bf2f(row[lane]), x2 = bf2f(row[lane + D / 2]);
+                            row[lane] = (uint16_t)f2bf(add_rn(mul_rn(x1, cv), mul_rn(-x2, sv)));
+                            row[lane + D / 2] = (uint16_t)f2bf(add_rn(mul_rn(x2, cv), mul_rn(x1, sv)));
+                        }
+                        // the unit holding the new position appends it to the cache
+                        if (au.lo <= T - 1 && T - 1 < au.hi) {
+                            uint16_t *kd = slp[l].kc + ((size_t)au.kvh * a.T_cap + (T - 1)) * D;
+                            uint16_t *vd = slp[l].vt + (size_t)au.kvh * D * a.T_cap + (T - 1);
+                            const uint16_t *kr = qkv_l + RMAX * D, *vr = qkv_l + RMAX * D + D;
+                            kd[lane] = kr[lane];
+                            kd[lane + 64] = kr[lane + 64];
+                            vd[(size_t)lane * a.T_cap] = vr[lane];
+                            vd[(size_t)(lane + 64) * a.T_cap] = vr[lane + 64];
+                        }
+                    }
+                }
+            } else if (k == K_MERGE) {
+                // attention output values [c0, c0 + C) of [H * D]: lane r < NR reads range r's
+                // (m, l) and its C values of O, then the ranges merge across lanes
+                const int C = a.C_merge;
+                const int c0 = wg * C;
+                if (c0 < a.H * D) {
+                    const int hq = c0 / D, d0 = c0 - hq * D;
+                    const int kvh = hq / a.R, hr = hq - kvh * a.R;
+                    const uint2 *src = a.buf[B_PART];
+                    const bool act = lane < a.NR;
+                    const size_t wb = ((size_t)(kvh * a.NR + min(lane, a.NR - 1)) * a.R + hr) * (D + 2);
+                    // word pairs: pair 0 = (m, l); pair i >= 1 = O values d0 + 2 (i - 1), + 1
+                    uint32_t pend = act ? ((2u << (C / 2)) - 1u) : 0u;
+                    float mv = -INFINITY, lv = 0.f, ov[16];
+#pragma unroll
+                    for (int d = 0; d < 16; ++d) ov[d] = 0.f;
+                    for (int it = 0;; ++it) {
+                        unsigned long long v[18];
+#pragma unroll
+                        for (int i = 0; i < 9; ++i) {
+                            const uint2 *p = src + wb + (i == 0 ? D : d0 + 2 * (i - 1));
+                            if (i <= C / 2) {
+                                v[2 * i] = ll_load(p);
+                                v[2 * i + 1] = ll_load(p + 1);
+                            } else {
+                                v[2 * i] = v[2 * i + 1] = 0ull;
+                            }
+                        }
+#pragma unroll
+                        for (int i = 0; i < 9; ++i) {
+                            if ((pend & (1u << i)) && (uint32_t)(v[2 * i] >> 32) == ep_in &&
+                                (uint32_t)(v[2 * i + 1] >> 32) == ep_in) {
+                                const float f0 = __uint_as_float((uint32_t)v[2 * i]);
+                                const float f1 = __uint_as_float((uint32_t)v[2 * i + 1]);
+                                if (i == 0) {
+                                    mv = f0;
+                                    lv = f1;
+                                } else {
+                                    ov[2 * (i - 1)] = f0;
+                                    ov[2 * (i - 1) + 1] = f1;
+                                }
+                                pend &= ~(1u << i);
+                            }
+                        }
+                        if (__ballot(pend != 0u) == 0ull) break;
+                        if ((it & 15) == 15 && (timed_out() ||
+                            __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
+                            ok = false;
+                            break;
+                        }
+                    }
+                    if (ok) {
+                        if (!act) {
+                            mv = -INFINITY;
+                            lv = 0.f;
+                        }
+                        const float M = lanes_max(mv);
+                        const float wr = (mv == -INFINITY) ? 0.f : exp2f(mv - M);
+                        const float L = lanes_sum(act ? wr * lv : 0.f);
+                        const float inv = 1.f / L;
+                        float lo = 0.f, hi = 0.f;                    // lane d / 2 keeps values d, d + 1
+#pragma unroll
+                        for (int d = 0; d < 16; d += 2) {
+                            if (d < C) {
+                                const float s0 = lanes_sum(act ? wr * ov[d] : 0.f);
+                                const float s1 = lanes_sum(act ? wr * ov[d + 1] : 0.f);
+                                if (2 * lane == d) {
+                                    lo = s0;
+                                    hi = s1;
+                                }
+                            }
+                        }
+                        if (lane < C / 2)
+                            ll_store(a.buf[B_ATT] + c0 / 2 + lane, pack_bf16x2(lo * inv, hi * inv), epoch(jj));
+                    }
+                }
+            }
+            if (!ok && lane == 0) s_abort = 1;
+        }
+        __syncthreads();                                             // B2: raw input staged
+        if (s_abort) {
+            __syncthreads();
+            return;
+        }
+        if (is_gemv) {
+            if (o.flags & F_NORM) {
+                // RMSNorm with add_rms_norm_kernel's partition: thread t < 256 sums chunks
+                // t, t + 256, ...; the 4 wave sums are added in order
+                if (tid < NORM_THREADS) {
+                    float ss = 0.f;
+                    for (int c = tid; c < W; c += NORM_THREADS) ss = sumsq_bf16x8(ss, hbuf[c]);
+                    ss = wave_sum(ss);
+                    if (lane == 0) s_red[wave] = ss;
+                }
+                __syncthreads();
+                float tot = 0.f;
+#pragma unroll
+                for (int i = 0; i < NORM_THREADS / 64; ++i) tot += s_red[i];
+                const float root = rms_root(tot, o.K, a.eps);
+                for (int c = tid; c < W; c += THREADS) put_x(c, norm_bf16x8(hbuf[c], xl[c], root));
+            } else {
+                for (int c = tid; c < W; c += THREADS) put_x(c, xl[c]);
+            }
+        }
+        __syncthreads();                                             // B3: op jj's input ready
+    };
+
+    // ====================================================================== item stream
+    // Stream item g of this workgroup -> (layer l, op kind k, item i of the op); its op
+    // index is 1 + NT l + k.  The prefixes live in registers and the division is a
+    // multiply-high, so an item is located without dependent LDS reads.
+    const int total = s_total;
+    const int ipl = s_pre[NT];                  // items per layer (> 0 when total > 0)
+    int pre[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) pre[k] = s_pre[k];
+    const unsigned ipl_magic = ipl > 1 ? (unsigned)((0x100000000ULL + (unsigned)ipl - 1) / (unsigned)ipl) : 0u;
+    int tbk[4];                                 // first tile of this workgroup per projection
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int te;
+        gemv_tiles(sgd[i].T, wg, P, tbk[i], te);
+    }
+    struct ItemLoc {
+        int l, k, i, ch;
+    };
+    // DMA of item g to LDS dst: 4 weight instructions + 1 scale/bias (or 4 key/value + 1
+    // filler) instructions.
+    auto dma_item = [&](int g, uint32_t dst) __attribute__((always_inline)) -> ItemLoc {
+        ItemLoc w;
+        w.l = ipl == 1 ? g : (int)__umulhi((unsigned)g, ipl_magic);     // g * ipl < 2^32
+        const int r = g - w.l * ipl;
+        int kind = 0, base_k = 0;
+#pragma unroll
+        for (int kk = 1; kk < NT; ++kk)
+            if (r >= pre[kk]) {
+                kind = kk;
+                base_k = pre[kk];
+            }
+        w.k = kind;
+        w.i = r - base_k;
+        w.ch = 0;
+        const LayerPtrs &lp = slp[w.l];
+        const uint32_t d1 = dst + 1024, d2 = dst + 2048, d3 = dst + 3072, d4 = dst + 4096;
+        if (w.k != K_ATTN) {
+            const int gi = gemv_index(w.k);
+            const GemvDesc &o = sgd[gi];
+            const int cpt = o.cpt;
+            const int tl = cpt == 1 ? w.i : (int)__umulhi((unsigned)w.i, o.cpt_magic);
+            const int ch = w.i - tl * cpt;
+            w.ch = ch;
+            const int n0 = (tbk[gi] + tl) * 16;
+            const uint32_t row_bytes = (uint32_t)o.K * BITS / 8;        // every weight matrix < 4 GB
+            const bool swiglu = o.flags & F_SWIGLU;
+            const int half = o.half, N = o.N;
+            const uint32_t G = (uint32_t)o.G;
+            auto wrow = [&](int rr) -> uint32_t {
+                if (swiglu) return (uint32_t)((rr < 8 ? 0 : half - 8) + (n0 >> 1) + rr);
+                return (uint32_t)min(n0 + rr, N - 1);
+            };
+            const uint8_t *wq = reinterpret_cast<const uint8_t *>(lp.wq[gi]) + ch * 256;
+            const uint32_t dq[4] = {dst, d1, d2, d3};
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int rr = 4 * q4 + (lane >> 4);
+                const int col = ((lane & 15) - rr) & 15;
+                dma16(wq + (wrow(rr) * row_bytes + (uint32_t)(col * 16)), dq[q4]);
+            }
+            if (lane < 32)
+                dma16((lane < 16 ? lp.s[gi] : lp.b[gi]) + (wrow(lane & 15) * G + (uint32_t)((ch * ITEM_GROUPS) & ~7)), d4);
+        } else {
+            // 8 cached keys: K rows [kb, kb + 8) (2 KB; row r's 16-byte chunks rotated by r, so
+            // the 8 rows' same chunk sits in different banks) and V^T columns (128 x 16 B)
+            const int kb = au.lo + 8 * w.i;
+            const uint8_t *kp = reinterpret_cast<const uint8_t *>(lp.kc + ((size_t)au.kvh * a.T_cap + kb) * D);
+            const uint16_t *vp = lp.vt + (size_t)au.kvh * D * a.T_cap + kb;
+            const int kr0 = lane >> 4, kr1 = 4 + (lane >> 4);
+            dma16(kp + kr0 * 256 + (((lane & 15) + kr0) & 15) * 16, dst);
+            dma16(kp + kr1 * 256 + (((lane & 15) + kr1) & 15) * 16, d1);
+            dma16(vp + (size_t)lane * a.T_cap, d2);
+            dma16(vp + (size_t)(64 + lane) * a.T_cap, d3);
+            if (lane < 32) dma16(kp + 16 * lane, d4);
+        }
+        return w;
+    };
+
+    if (ctl) {
+        for (int jj = 0; jj <= nops; ++jj) boundary(jj);
+        if (lane == 0 && s_abort) atomicOr(a.status, 2u);
+        if (wg == 0 && lane == 0) {
+            // every workgroup read the base before producing anything, and workgroup 0
+            // ends after consuming every workgroup's outputs of the last gate|up
+            a.epoch_base[0] = base + 1u;
+        }
+        return;
+    }
+
+    {
+        // ================================================================ worker
+        uint8_t *ring = smem + (size_t)wave * TRING * SLOT;
+        const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
+
+        // per ring slot: op index, op kind, item of the op, and (projections) its K chunk
+        int sj[TRING], sk[TRING], si[TRING], sch[TRING];
+        // DMA of item g into ring slot `slot`
+        auto issue = [&](int g, int slot) {
+            const ItemLoc w = dma_item(min(g, total - 1), ring_lds + slot * SLOT);
+            sj[slot] = 1 + NT * w.l + w.k;
+            sk[slot] = w.k;
+            si[slot] = w.i;
+            sch[slot] = w.ch;
+        };
+
+        // ---- projection item (the math of qgemv_m1_kernel)
+        const int j16 = lane & 15, q = lane >> 4;
+        const bool a_zero = BITS == 4 && ((j16 == 0 && q >= 2) || (j16 == 8 && q < 2));
+        const int epar = BITS == 4 ? (q >> 1) : 0;
+        const int xq = BITS == 4 ? 4 * q : 2 * q;
+        uint32_t magic = 0x43004300u;
+        asm volatile("" : "+v"(magic));
+        uint32_t nib_mask = 0x000F000Fu;
+        asm volatile("" : "+s"(nib_mask));
+
+        auto gemv_item = [&](int ch, int i, int slot) {
+            const uint4 *sl = reinterpret_cast<const uint4 *>(ring + slot * SLOT);
+            uint4 wv[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) wv[t] = sl[(j16 >> 2) * 64 + (j16 & 3) * 16 + ((4 * t + q + j16) & 15)];
+            const uint4 sv = sl[4096 / 16 + j16];
+            const uint4 bv = sl[4096 / 16 + 16 + j16];
+            const int gsub = (ch * ITEM_GROUPS) & 7;
+            const uint4 *xrow = a_zero ? xzero : xl + ch * 4 * SPAN_WORDS;
+            float xsv[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xsv[t] = xs[(ch * 4 + t) * SPAN_GROUPS + epar];
+            f4 P4[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) P4[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < MFMAS; ++u) {
+                // x for this step of the four chains (loaded per step: registers are short)
+                uint4 xa[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xa[t] = xrow[t * SPAN_WORDS + xq + u];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    bf16x8_t Bv;
+                    if (BITS == 4) {
+                        const uint32_t w = wc(wv[t], u);
+                        Bv = as_bf16x8(and_or(w, nib_mask, magic), and_or(w >> 4, nib_mask, magic),
+                                       and_or(w >> 8, nib_mask, magic), and_or(w >> 12, nib_mask, magic));
+                    } else {
+                        const uint32_t w0 = wc(wv[t], 2 * u), w1 = wc(wv[t], 2 * u + 1);
+                        Bv = as_bf16x8(byte_pair_lo(w0), byte_pair_hi(w0), byte_pair_lo(w1), byte_pair_hi(w1));
+                    }
+                    P4[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[t]), Bv, P4[t], 0, 0, 0);
+                }
+            }
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int gsel = gsub + t * SPAN_GROUPS + epar;
+                const float sf = bf2f(wh(sv, gsel));
+                const float bf = bf2f(wh(bv, gsel));
+                const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
+                acc = fmaf(sf, P4[t][0], fmaf(cf, xsv[t], acc));
+            }
+            if (BITS == 4) acc += __shfl_xor(acc, 32);
+            if (q == 0) part[i * 16 + j16] = acc;
+        };
+
+        // ---- attention item: 8 keys; lane = (key k = lane / 8, dims [16 sg, 16 sg + 16))
+        const int akey = lane >> 3, asg = lane & 7;
+        const int R = a.R;
+        // item i's softmax state over its 8 keys (m, l per head; O for dims lane and
+        // lane + 64) goes to state block i; the op's epilogue merges the blocks in order
+        auto attn_item = [&](int i, int slot) {
+            float *stw = ast + i * AST;
+            float am[RMAX], al[RMAX], ao[RMAX][2];
+            const uint8_t *sl = ring + slot * SLOT;
+            const int kb = au.lo + 8 * i;
+            const int kpos = kb + akey;
+            const bool kvalid = kpos < au.hi;
+            const int newk = T - 1 - kb;                       // the new key's index in this block, if in 0..7
+            // the new key is not in the cache yet: its rotated copy sits in LDS (unrotated
+            // layout); cached key chunk c of row k is at slot (c - k) & 15
+            uint4 k0, k1;
+            if (kpos == T - 1) {
+                const uint4 *kn = reinterpret_cast<const uint4 *>(qkv_l + RMAX * D) + 2 * asg;
+                k0 = kn[0];
+                k1 = kn[1];
+            } else {
+                const uint4 *kr = reinterpret_cast<const uint4 *>(sl + akey * 256);
+                k0 = kr[(2 * asg - akey) & 15];
+                k1 = kr[(2 * asg + 1 - akey) & 15];
+            }
+            float sc[RMAX];
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r < R) {
+                    const uint4 *qp = reinterpret_cast<const uint4 *>(qkv_l + r * D) + 2 * asg;
+                    const uint4 q0 = qp[0], q1 = qp[1];
+                    float d = 0.f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(bfe(q0, e), bfe(k0, e), d);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d = fmaf(bfe(q1, e), bfe(k1, e), d);
+                    d = group8_sum(d);
+                    sc[r] = kvalid ? d * a.scale_log2 : -INFINITY;
+                } else {
+                    sc[r] = -INFINITY;
+                }
+            }
+            float p[RMAX];
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                const float bm = groups_max(sc[r]);
+                p[r] = (sc[r] == -INFINITY) ? 0.f : exp2f(sc[r] - bm);
+                al[r] = groups_sum(p[r]);
+                am[r] = bm;
+                ao[r][0] = 0.f;
+                ao[r][1] = 0.f;
+            }
+            // O += P V over the valid keys of the block; lane dims lane and lane + 64 (V^T rows
+            // of 16 B: 16 lanes read 256 contiguous bytes)
+            const uint4 va = *reinterpret_cast<const uint4 *>(sl + 2048 + lane * 16);
+            const uint4 vb = *reinterpret_cast<const uint4 *>(sl + 2048 + (lane + 64) * 16);
+            const uint32_t vn0 = qkv_l[RMAX * D + D + lane], vn1 = qkv_l[RMAX * D + D + lane + 64];
+            const int nval = min(8, au.hi - kb);               // wave-uniform
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                if (kk < nval) {
+                    float fa = bfe(va, kk), fb = bfe(vb, kk);
+                    if (kk == newk) {
+                        fa = __uint_as_float(vn0 << 16);
+                        fb = __uint_as_float(vn1 << 16);
+                    }
+#pragma unroll
+                    for (int r = 0; r < RMAX; ++r) {
+                        const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[r]), 8 * kk));
+                        ao[r][0] = fmaf(pk, fa, ao[r][0]);
+                        ao[r][1] = fmaf(pk, fb, ao[r][1]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (lane == 0) {
+                    stw[r * (D + 2) + D] = am[r];
+                    stw[r * (D + 2) + D + 1] = al[r];
+                }
+                stw[r * (D + 2) + lane] = ao[r][0];
+                stw[r * (D + 2) + lane + 64] = ao[r][1];
+            }
+        };
+
+        // Every op boundary up to and including op k's staging, before the item of op
+        // k is awaited: the other waves need not wait for this wave's next DMA.
+        int staged = 0;
+        auto catch_up = [&](int k) __attribute__((always_inline)) {
+            while (staged <= k) {
+                boundary(staged);
+                ++staged;
+            }
+        };
+        auto compute = [&](int slot) {
+            if (sk[slot] == K_ATTN) attn_item(si[slot], slot);
+            else gemv_item(sch[slot], si[slot], slot);
+        };
+        auto claim = [&]() -> int {
+            int v = 0;
+            if (lane == 0) v = atomicAdd(&s_ctr, 1);
+            return __builtin_amdgcn_readfirstlane(v);
+        };
+
+        if (total > 0) {
+            // slot s holds item held[s]; TRING - 1 items in flight while one is computed
+            int held[TRING];
+#pragma unroll
+            for (int s = 0; s < TRING - 1; ++s) {
+                held[s] = wave + WORKERS * s;
+                issue(held[s], s);
+            }
+            bool more = true;
+            while (more) {
+#pragma unroll
+                for (int s = 0; s < TRING; ++s) {
+                    if (more) {
+                        const int nx = (s + TRING - 1) % TRING;
+                        held[nx] = claim();
+                        issue(held[nx], nx);
+                        if (held[s] >= total) {
+                            more = false;
+                        } else {
+                            catch_up(sj[s]);
+                            if (s_abort) {
+                                more = false;
+                            } else {
+                                wait_vm<DMA_PER_ITEM * (TRING - 1)>();
+                                compute(s);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        catch_up(nops);                                 // the remaining boundaries, the last one finishing the step
+        wait_vm<0>();                                   // no DMA may land after the workgroup ends
+    }
+}
+
+// ---------------------------------------------------------------- host side
+
+struct DecodePlan {
+    int device = 0;
+    int bits = 4;
+    int P = 0;
+    Args args{};
+    LayerPtrs *d_layers = nullptr;
+    void *d_mem = nullptr;      // exchange buffers, epoch base, status
+    size_t lds = 0;
+};
+
+static size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, void **out) {
+    if (!m || !layers || !out) return set_error(SC_EINVAL, "decode_plan: null argument");
+    *out = nullptr;
+    const int L = m->num_layers, hid = m->hidden, I = m->intermediate, H = m->num_heads, Hkv = m->num_kv_heads,
+              D = m->head_dim;
+    if (m->bits != 4 && m->bits != 8) return set_error(SC_EUNSUPPORTED, "decode_plan: bits must be 4 or 8");
+    if (m->group_size != 64) return set_error(SC_EUNSUPPORTED, "decode_plan: group size 64 only");
+    if (D != HD) return set_error(SC_EUNSUPPORTED, "decode_plan: head_dim %d (128 only)", D);
+    if (L <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || H / Hkv > RMAX)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: at most %d query heads per kv head", RMAX);
+    if (hid % 512 || I % 512 || (H * D) % 512)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: widths must be multiples of 512");
+    if (hid > 16384 || I > 16384 || H * D > 16384)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: widths up to 16384");
+    if (m->T_cap <= 0 || m->T_cap % 32) return set_error(SC_EINVAL, "decode_plan: cache capacity must be a multiple of 32");
+    if (!m->counters || !m->ids || !m->embed || !m->cos_t || !m->sin_t || !m->h_out)
+        return set_error(SC_EINVAL, "decode_plan: null model pointer");
+    if (m->vocab_local <= 0 || m->vocab_local >= (1L << 31) || m->table_len <= 0 || m->pos_offset < 0)
+        return set_error(SC_EINVAL, "decode_plan: bad vocabulary or rotary table");
+    int dev = 0;
+    SC_HIP_CHECK(hipGetDevice(&dev));
+    const DeviceInfo &di = device_info();
+    const int P = di.num_cus;
+    if (P < 8 || P > 4096) return set_error(SC_EUNSUPPORTED, "decode_plan: %d CUs", P);
+    const int R = H / Hkv;
+    const int NR = P / Hkv;
+    if (NR < 1 || NR > 64) return set_error(SC_EUNSUPPORTED, "decode_plan: %d kv heads on %d CUs", Hkv, P);
+    const int C = (H * D) / P;
+    if ((H * D) % P || C < 2 || C % 2 || C > 16 || D % C)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: attention rows do not split over %d CUs", P);
+    const int qkvN = (H + 2 * Hkv) * D;
+
+    Args a{};
+    auto desc = [&](int N, int K, int flags, int in_buf, int out_buf) {
+        GemvDesc g{};
+        g.N = N; g.K = K; g.G = K / 64;
+        g.T = (flags & F_SWIGLU) ? N / 16 : (N + 15) / 16;
+        g.cpt = K / (m->bits == 4 ? 512 : 256);
+        g.cpt_magic = g.cpt > 1 ? (unsigned)((0x100000000ULL + (unsigned long long)g.cpt - 1) / (unsigned long long)g.cpt) : 0u;
+        g.half = (flags & F_SWIGLU) ? N / 2 : 0;
+        g.flags = flags; g.in_buf = in_buf; g.out_buf = out_buf;
+        return g;
+    };
+    a.gd[0] = desc(qkvN, hid, F_NORM, B_H, B_QKV);
+    a.gd[1] = desc(hid, H * D, F_RESID, B_ATT, B_HMID);
+    a.gd[2] = desc(2 * I, hid, F_NORM | F_SWIGLU, B_HMID, B_ACT);
+    a.gd[3] = desc(hid, I, F_RESID, B_ACT, B_H);
+
+    std::vector<LayerPtrs> lps(L);
+    for (int l = 0; l < L; ++l) {
+        const sc_decode_layer &y = layers[l];
+        LayerPtrs &p = lps[l];
+        p.wq[0] = y.wq_qkv; p.s[0] = y.s_qkv; p.b[0] = y.b_qkv;
+        p.wq[1] = y.wq_o; p.s[1] = y.s_o; p.b[1] = y.b_o;
+        p.wq[2] = y.wq_gu; p.s[2] = y.s_gu; p.b[2] = y.b_gu;
+        p.wq[3] = y.wq_down; p.s[3] = y.s_down; p.b[3] = y.b_down;
+        p.ln[0] = y.ln_in; p.ln[1] = y.ln_post;
+        p.kc = y.kc; p.vt = y.vt;
+        for (int i = 0; i < 4; ++i)
+            if (!p.wq[i] || !p.s[i] || !p.b[i] || (((uintptr_t)p.wq[i] | (uintptr_t)p.s[i] | (uintptr_t)p.b[i]) % 16))
+                return set_error(SC_EINVAL, "decode_plan: layer %d: null or misaligned weights", l);
+        if (!p.ln[0] || !p.ln[1] || (((uintptr_t)p.ln[0] | (uintptr_t)p.ln[1]) % 16) || !p.kc || !p.vt ||
+            (((uintptr_t)p.kc | (uintptr_t)p.vt) % 16))
+            return set_error(SC_EINVAL, "decode_plan: layer %d: null or misaligned norm/cache pointers", l);
+    }
+
+    // LDS layout
+    const int Kmax = std::max({hid, I, H * D});
+    int max_items = 0;
+    for (int i = 0; i < 4; ++i) {
+        const int tiles = (a.gd[i].T + P - 1) / P;
+        max_items = std::max(max_items, tiles * a.gd[i].cpt);
+    }
+    size_t off = (size_t)WORKERS * TRING * SLOT;
+    // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 2) floats
+    const int kps_max = ((m->T_cap + NR - 1) / NR + 7) & ~7;
+    const size_t ast_bytes = (size_t)(kps_max / 8) * RMAX * (D + 2) * 4;
+    a.o_xl = (int)off; off += align16(std::max((size_t)Kmax * 2, ast_bytes));
+    a.o_xzero = (int)off; off += 1024;
+    a.o_xs = (int)off; off += align16((size_t)(Kmax / 64) * 4);
+    // projection partials, or the attention merge [RMAX][D + 2]
+    a.o_part = (int)off; off += align16(std::max((size_t)max_items * 64, (size_t)RMAX * (D + 2) * 4));
+    a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
+    a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
+    a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
+    a.o_lp = (int)off; off += (size_t)L * sizeof(LayerPtrs);
+    a.lds_bytes = (int)off;
+    const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
+    if (off + 128 > (size_t)lds_cap)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: needs %zu bytes of LDS (limit %d)", off, lds_cap);
+
+    // device memory: layer table, exchange buffers, epoch base, status
+    const size_t nb_h = (size_t)hid / 2, nb_qkv = (size_t)qkvN / 2, nb_part = (size_t)Hkv * NR * R * (D + 2),
+                 nb_att = (size_t)H * D / 2, nb_act = (size_t)I / 2;
+    const size_t words[B_COUNT] = {nb_h, nb_qkv, nb_part, nb_att, nb_h, nb_act};
+    size_t mem = 256;
+    size_t boff[B_COUNT];
+    for (int i = 0; i < B_COUNT; ++i) {
+        boff[i] = mem;
+        mem += ((words[i] * 8 + 255) / 256) * 256;
+    }
+    std::unique_ptr<DecodePlan> pl(new DecodePlan());
+    pl->device = dev;
+    pl->bits = m->bits;
+    pl->P = P;
+    pl->lds = off;
+    SC_HIP_CHECK(hipMalloc(&pl->d_mem, mem));
+    SC_HIP_CHECK(hipMemset(pl->d_mem, 0, mem));
+    SC_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&pl->d_layers), (size_t)L * sizeof(LayerPtrs)));
+    SC_HIP_CHECK(hipMemcpy(pl->d_layers, lps.data(), (size_t)L * sizeof(LayerPtrs), hipMemcpyHostToDevice));
+    uint8_t *mb = static_cast<uint8_t *>(pl->d_mem);
+    const uint32_t one = 1;
+    SC_HIP_CHECK(hipMemcpy(mb, &one, 4, hipMemcpyHostToDevice));   // epoch base starts at 1
+    a.layers = pl->d_layers;
+    for (int i = 0; i < B_COUNT; ++i) a.buf[i] = reinterpret_cast<uint2 *>(mb + boff[i]);
+    a.counters = m->counters;
+    a.epoch_base = reinterpret_cast<uint32_t *>(mb);
+    a.status = reinterpret_cast<unsigned *>(mb + 64);
+    a.ids = m->ids;
+    a.embed = m->embed;
+    a.cos_t = m->cos_t;
+    a.sin_t = m->sin_t;
+    a.h_out = m->h_out;
+    a.vocab_start = m->vocab_start;
+    a.V_local = (int)m->vocab_local;
+    a.table_len = m->table_len;
+    a.pos_offset = m->pos_offset;
+    a.L = L;
+    a.nops = 1 + NT * L;
+    a.hidden = hid;
+    a.H = H; a.Hkv = Hkv; a.R = R; a.NR = NR; a.T_cap = m->T_cap;
+    a.C_merge = C;
+    a.eps = m->eps;
+    a.scale_log2 = m->scale * 1.4426950408889634f;
+    pl->args = a;
+    SC_HIP_CHECK(hipDeviceSynchronize());
+    *out = pl.release();
+    return SC_OK;
+}
+
+int decode_plan_run(void *plan, hipStream_t stream) {
+    DecodePlan *pl = static_cast<DecodePlan *>(plan);
+    if (!pl) return set_error(SC_EINVAL, "decode_plan_run: null plan");
+    int dev = 0;
+    SC_HIP_CHECK(hipGetDevice(&dev));
+    if (dev != pl->device) return set_error(SC_EINVAL, "decode_plan_run: plan belongs to device %d", pl->device);
+    auto go = [&](auto kern) -> int {
+        static int configured[2] = {0, 0};
+        int &cfg = configured[pl->bits == 4 ? 0 : 1];
+        if ((int)pl->lds > cfg) {
+            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl->lds));
+            cfg = (int)pl->lds;
+        }
+        int occ = 0;
+        SC_HIP_CHECK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, reinterpret_cast<const void *>(kern), THREADS,
+                                                                  pl->lds));
+        if (occ < 1) return set_error(SC_EUNSUPPORTED, "decode_plan_run: kernel does not fit on a CU");
+        hipLaunchKernelGGL(kern, dim3(pl->P), dim3(THREADS), pl->lds, stream, pl->args);
+        SC_HIP_CHECK(hipGetLastError());
+        return SC_OK;
+    };
+    if (pl->bits == 4) return go(decode_step_kernel<4>);
+    return go(decode_step_kernel<8>);
+}
+
+int decode_plan_status(void *plan, unsigned *status) {
+    DecodePlan *pl = static_cast<DecodePlan *>(plan);
+    if (!pl || !status) return set_error(SC_EINVAL, "decode_plan_status: null argument");
+    SC_HIP_CHECK(hipMemcpy(status, pl->args.status, 4, hipMemcpyDeviceToHost));
+    return SC_OK;
+}
+
+void decode_plan_destroy(void *plan) {
+    DecodePlan *pl = static_cast<DecodePlan *>(plan);
+    if (!pl) return;
+    (void)hipFree(pl->d_layers);
+    (void)hipFree(pl->d_mem);
+    delete pl;
+}
+
+}  // namespace sc

@@ -26,6 +26,7 @@ from typing import Any, Callable, Dict, List, Optional
 import torch
 
 from . import _lib
+from .decode_plan import maybe_plan
 from .kv_cache import KVCache, round_capacity
 from .parallel.transformer import ParallelTransformer, StepBuffers, run_sync
 
@@ -80,11 +81,14 @@ TokenCallback = Callable[[int, int, bool], Any]
 class DecodeGraph:
     """One greedy decode step of ``model`` for ``batch`` sequences, as a replayable graph."""
 
-    def __init__(self, model: ParallelTransformer, cache: KVCache, tokens: torch.Tensor, use_graph: bool = True):
+    def __init__(self, model: ParallelTransformer, cache: KVCache, tokens: torch.Tensor, use_graph: bool = True,
+                 fused_trunk: bool = True):
         self.model = model
         self.cache = cache
         self.tokens = tokens
         self.bufs = StepBuffers(model, cache.batch, 1, cache.capacity)
+        if fused_trunk:
+            self.bufs.plan = maybe_plan(model, cache, self.bufs.ids, self.bufs.h)
         self.use_graph = use_graph
         self.graph = None
         self.logits = None

@@ -165,6 +165,7 @@ class StepBuffers:
         if S == 1:
             ws = max(ws, _lib.attention_decode_workspace_bytes(B, H, Hk, D, T_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.plan = None          # a TrunkPlan when the whole trunk runs as one launch
 
 
 class ParallelTransformer:
@@ -313,11 +314,11 @@ class ParallelTransformer:
         return h, pending
 
     async def _head(self, h, pending, B, S, last_only, hn_out=None):
-        if pending is None:
-            pending = torch.zeros_like(h)
+        """Final RMSNorm (of h + pending, when a residual add is pending) and lm_head."""
         if last_only and S > 1:
             h = h.reshape(B, S, -1)[:, -1].contiguous()
-            pending = pending.reshape(B, S, -1)[:, -1].contiguous()
+            if pending is not None:
+                pending = pending.reshape(B, S, -1)[:, -1].contiguous()
         lm = self.lm_head
         if isinstance(lm, QuantizedColumnParallelLinear):
             if lm.quantized_weight is None:
@@ -379,8 +380,12 @@ class ParallelTransformer:
         logits into ``bufs.ids`` and ``tokens[:, step]``, then advance the cache
         length and the step counter.  Captured once, replayed per token."""
         B = bufs.B
-        h = self._embed_sync(bufs.ids, out=bufs.h.view(B, 1, self.hidden_size)).view(B, self.hidden_size)
-        h, pending = run_sync(self._trunk(h, cache, B, 1, bufs))
+        if bufs.plan is not None:
+            # embedding and every layer in one persistent launch (batch 1)
+            h, pending = bufs.plan.run().view(B, self.hidden_size), None
+        else:
+            h = self._embed_sync(bufs.ids, out=bufs.h.view(B, 1, self.hidden_size)).view(B, self.hidden_size)
+            h, pending = run_sync(self._trunk(h, cache, B, 1, bufs))
         logits = run_sync(self._head(h, pending, B, 1, True, hn_out=bufs.hn))
         _lib.argmax(logits.reshape(B, -1), ids=bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
         _lib.add_i32(cache.counters, 1, n=2)
