@@ -39,6 +39,8 @@
 #include <memory>
 #include <vector>
 
+#include <type_traits>
+
 #include "dma_util.h"
 #include "../../include/shardcompute_hip.h"
 
@@ -71,6 +73,8 @@ struct GemvDesc {
     unsigned cpt_magic;     // ceil(2^32 / cpt): item / cpt == umulhi(item, cpt_magic)
     int half;               // F_SWIGLU: output width (gate rows)
     int flags, in_buf, out_buf;
+    const uint2 *in;        // LL words of the input and the output (exchange buffers in_buf, out_buf)
+    uint2 *out;
 };
 
 // Device pointers of one layer: projections q|k|v, o, gate|up, down; norms; cache.
@@ -98,6 +102,7 @@ struct Args {
     int L, nops, hidden, H, Hkv, R, NR, T_cap, C_merge;
     float eps, scale_log2;
     // LDS layout (byte offsets into dynamic shared memory)
+    int n_items;            // attention items per unit at most (keys per unit / 8)
     int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
 };
 
@@ -123,35 +128,6 @@ __device__ __forceinline__ int gemv_index(int kind) {
     return kind == K_QKV ? 0 : kind == K_O ? 1 : kind == K_GU ? 2 : 3;
 }
 
-// Lane reductions on the VALU: DPP moves within rows of 16 lanes and the permlane
-// swaps across rows, no LDS round trip.  Each step adds (or maxes) two operands, so
-// every lane of a group ends with the same bits.
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int DPP_XOR1 = 0xB1;          // quad_perm [1, 0, 3, 2]
-constexpr int DPP_XOR2 = 0x4E;          // quad_perm [2, 3, 0, 1]
-constexpr int DPP_HALF_MIRROR = 0x141;  // lane i of 8 <- lane 7 - i
-constexpr int DPP_ROR8 = 0x128;         // lane i of 16 <- lane (i + 8) mod 16
-// (rows 0 1 2 3) -> a = (r0 r0 r2 r2), b = (r1 r1 r3 r3)
-__device__ __forceinline__ void swap16(float v, float &a, float &b) {
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    a = __uint_as_float(p[0]);
-    b = __uint_as_float(p[1]);
-}
-// (lanes 0-31, 32-63) -> a = (lo lo), b = (hi hi)
-__device__ __forceinline__ void swap32(float v, float &a, float &b) {
-    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    a = __uint_as_float(p[0]);
-    b = __uint_as_float(p[1]);
-}
-// sum over the 8 lanes 8g .. 8g + 7
-__device__ __forceinline__ float group8_sum(float v) {
-    v += dpp_mov<DPP_XOR1>(v);
-    v += dpp_mov<DPP_XOR2>(v);
-    return v + dpp_mov<DPP_HALF_MIRROR>(v);
-}
 // v equal within each group of 8 lanes: sum / max over the 8 groups
 __device__ __forceinline__ float groups_sum(float v) {
     float a, b;
@@ -201,7 +177,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     constexpr int ITEM_GROUPS = ITEM_K / 64;
     constexpr int MFMAS = BITS == 4 ? 4 : 2;
     constexpr int D = HD;
-    constexpr int AST = RMAX * (D + 2);     // floats per attention item state
+    constexpr int AST = RMAX * (D + 4);     // floats per attention item state: [RMAX][D + 4] = O, m, l, pad
 
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int s_ctr;                   // next stream item to claim
@@ -283,7 +259,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     // partials and publishes its output) and stages op jj's input in LDS.  The control
     // wave publishes, polls narrow inputs and appends to the cache; every wave polls
     // wide inputs.  __syncthreads waits on LDS only.
-    const bool ctl = wave == CTL;
+
     const unsigned long long t_start = now();
     auto timed_out = [&]() -> bool {
         if (now() - t_start > TIMEOUT_TICKS) {
@@ -352,6 +328,10 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         return true;
     };
 
+    // the wait limit without recording it (the workers' copy: the control wave sets the
+    // status word for an aborted launch)
+    auto expired = [&]() -> bool { return now() - t_start > TIMEOUT_TICKS; };
+
     // Every wave: gather the raw chunks of a wide input (chunk c = LL words [4c, 4c + 4) of
     // src) into x, the blocks of 64 chunks dealt round-robin to the nine waves (at most 4
     // per wave).  Chunks that are not all there are then watched through their last word
@@ -400,11 +380,11 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 }
                 if (__ballot(fetch != 0u) != 0ull) break;
                 __builtin_amdgcn_s_sleep(2);
-                if ((sp & 15) == 15 && (timed_out() ||
+                if ((sp & 15) == 15 && (expired() ||
                     __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
                     return false;
             }
-            if ((it & 15) == 15 && (timed_out() ||
+            if ((it & 15) == 15 && (expired() ||
                 __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
                 return false;
         }
@@ -417,16 +397,17 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         float g = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) g += bfe(v, e);
-        g += __shfl_xor(g, 1);
-        g += __shfl_xor(g, 2);
-        g += __shfl_xor(g, 4);
+        g = group8_sum(g);
         if ((c & 7) == 0) xs[c >> 3] = g;
     };
 
     auto epoch = [&](int j) -> uint32_t { return base * (uint32_t)nops + (uint32_t)j + 1u; };
     auto kind_of = [&](int j) -> int { return j == 0 ? -1 : (j - 1) % NT; };
 
-    auto boundary = [&](int jj) __attribute__((always_inline)) {
+    // is_ctl: std::true_type in the control wave's copy, std::false_type in the
+    // workers' (the control wave's polls then cost the workers no registers)
+    auto boundary = [&](int jj, auto is_ctl) __attribute__((always_inline)) {
+        constexpr bool ctl = decltype(is_ctl)::value;
         __syncthreads();                                             // B1: op jj - 1 computed
         const int jp = jj - 1;
         // ------------------------------------------------------------ finish op jp
@@ -438,29 +419,34 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 if (au.valid) {
                     // merge the items' (m, l, O) per head, in item order (the same sums
                     // whichever wave computed which item), into part: [R][D + 2] = O
-                    // (unnormalised), m, l
+                    // (unnormalised), m, l.  First each item's weight exp2(m_i - M) per
+                    // head (fac[h][i], M at mh[h]), then one fma per item and value.
                     const int ni = au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
-                    for (int t = tid; t < a.R * (D + 2); t += THREADS) {
-                        const int h = t / (D + 2), x = t - h * (D + 2);
+                    uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
+                    float *fac = part + RMAX * (D + 2), *mh = fac + RMAX * a.n_items;
+                    for (int t = tid; t < a.R * ni; t += THREADS) {
+                        const int h = t / ni, w = t - h * ni;
                         float M = -INFINITY;
-                        for (int w = 0; w < ni; ++w) M = fmaxf(M, ast[w * AST + h * (D + 2) + D]);
-                        float acc = 0.f;
-                        for (int w = 0; w < ni; ++w) {
-                            const float mw = ast[w * AST + h * (D + 2) + D];
-                            if (mw != -INFINITY) {
-                                const float e = exp2f(mw - M);
-                                if (x == D) acc = M;
-                                else if (x == D + 1) acc = fmaf(e, ast[w * AST + h * (D + 2) + D + 1], acc);
-                                else acc = fmaf(e, ast[w * AST + h * (D + 2) + x], acc);
-                            }
-                        }
-                        part[t] = (x == D) ? M : acc;
+                        for (int v = 0; v < ni; ++v) M = fmaxf(M, ast[v * AST + h * (D + 4) + D]);
+                        const float mw = ast[w * AST + h * (D + 4) + D];
+                        fac[h * ni + w] = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+                        if (w == 0) mh[h] = M;
                     }
                     __syncthreads();
-                    if (ctl) {
-                        uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
-                        for (int t = lane; t < a.R * (D + 2); t += 64) ll_store(dst + t, __float_as_uint(part[t]), ep);
+                    for (int t = tid; t < a.R * (D + 2); t += THREADS) {
+                        const int h = t / (D + 2), x = t - h * (D + 2);
+                        float acc = 0.f;
+                        if (x == D) {
+                            acc = ni > 0 ? mh[h] : -INFINITY;
+                        } else {
+                            const float *src = ast + h * (D + 4) + x;          // x = D + 1: l
+                            for (int w = 0; w < ni; ++w) acc = fmaf(fac[h * ni + w], src[w * AST], acc);
+                        }
+                        part[t] = acc;
                     }
+                    __syncthreads();
+                    if (ctl)
+                        for (int t = lane; t < a.R * (D + 2); t += 64) ll_store(dst + t, __float_as_uint(part[t]), ep);
                 }
             } else if (kp != K_MERGE && ctl) {
                 if (jp == 0) {
@@ -479,7 +465,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     int tb, te;
                     gemv_tiles(o.T, wg, P, tb, te);
                     const int ntl = te - tb, cpt = o.cpt;
-                    uint2 *dst = a.buf[o.out_buf];
+                    uint2 *dst = o.out;
                     uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
                     if (o.flags & F_SWIGLU) {
                         // tile tl: gate columns 8 (tb + tl) + c, c < 8; 4 words per tile
@@ -532,11 +518,14 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         const int W = o.K >> 3;
         const bool wide = is_gemv && !(o.flags & F_NORM) && W > 512;     // every wave polls
         if (wide && !s_abort) {
-            if (!gather_all(a.buf[o.in_buf], W, ep_in) && lane == 0) s_abort = 1;
+            if (!gather_all(o.in, W, ep_in) && lane == 0) s_abort = 1;
+            // the workers' poll loads retire behind their weight DMA: retire them here,
+            // so that no wait for them is left at the join for the other ops' paths
+            wait_vm<0>();
         } else if (ctl && !s_abort) {
             bool ok = true;
             if (is_gemv) {
-                const uint2 *src = a.buf[o.in_buf];
+                const uint2 *src = o.in;
                 auto addr = [&](int c) -> const uint2 * { return src + 4 * (size_t)c; };
                 if (o.flags & F_NORM) {
                     // the norm weight lands in x's LDS (chunk c at x[c]) while the input is
@@ -775,8 +764,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         return w;
     };
 
-    if (ctl) {
-        for (int jj = 0; jj <= nops; ++jj) boundary(jj);
+    if (wave == CTL) {
+        for (int jj = 0; jj <= nops; ++jj) boundary(jj, std::true_type{});
         if (lane == 0 && s_abort) atomicOr(a.status, 2u);
         if (wg == 0 && lane == 0) {
             // every workgroup read the base before producing anything, and workgroup 0
@@ -856,92 +845,124 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
                 acc = fmaf(sf, P4[t][0], fmaf(cf, xsv[t], acc));
             }
-            if (BITS == 4) acc += __shfl_xor(acc, 32);
+            if (BITS == 4) acc = xor32_sum(acc);
             if (q == 0) part[i * 16 + j16] = acc;
         };
 
-        // ---- attention item: 8 keys; lane = (key k = lane / 8, dims [16 sg, 16 sg + 16))
-        const int akey = lane >> 3, asg = lane & 7;
+        // ---- attention item: 8 keys of kv head au.kvh against its R query heads, on MFMA
+        //   S^T[16 key rows (8 used) x 16 head columns (R used)] = K . Q^T   (4 x 16x16x32)
+        //   p = exp2(S^T scale - max), per head over the 8 keys (fp32; l sums fp32 p)
+        //   O^T[D x 16 heads] = V^T[D x keys] . P^T with P in bf16     (8 x 16x16x32)
+        // as the per-op attention kernel computes a block.  The item's (m, l, O) per head
+        // goes to state block i ([RMAX][D + 4] floats); the op's epilogue merges the
+        // blocks in item order, so the sums do not depend on which wave took which item.
+        // ac: MFMA column (key row of A, head column of B), ag: its k group.
         const int R = a.R;
-        // item i's softmax state over its 8 keys (m, l per head; O for dims lane and
-        // lane + 64) goes to state block i; the op's epilogue merges the blocks in order
         auto attn_item = [&](int i, int slot) {
+            // recomputed per item: hoisted out of the item loop, the per-tile addresses
+            // would be held (and spilled) across the whole stream
+            int ac = lane & 15;
+            asm volatile("" : "+v"(ac));
+            const int ag = lane >> 4;
             float *stw = ast + i * AST;
-            float am[RMAX], al[RMAX], ao[RMAX][2];
             const uint8_t *sl = ring + slot * SLOT;
             const int kb = au.lo + 8 * i;
-            const int kpos = kb + akey;
-            const bool kvalid = kpos < au.hi;
-            const int newk = T - 1 - kb;                       // the new key's index in this block, if in 0..7
-            // the new key is not in the cache yet: its rotated copy sits in LDS (unrotated
-            // layout); cached key chunk c of row k is at slot (c - k) & 15
-            uint4 k0, k1;
-            if (kpos == T - 1) {
-                const uint4 *kn = reinterpret_cast<const uint4 *>(qkv_l + RMAX * D) + 2 * asg;
-                k0 = kn[0];
-                k1 = kn[1];
+            const int nval = min(8, au.hi - kb);               // valid keys of the block, wave-uniform
+            const int newk = T - 1 - kb;                       // the new key's slot in the block, if 0..7
+            const bool has_new = newk >= 0 && newk < 8;        // wave-uniform
+            // operand A: key row ac, chunk 4u + ag (cached row r's chunk c sits at slot
+            // (c - r) & 15; rows 8..15 read the block's V^T bytes: their S rows are
+            // masked, and MFMA rows do not mix).  The new key is not in the cache yet:
+            // its rotated copy is in LDS.  Operand B: query head min(ac, R - 1), the same
+            // chunk (columns past R are ignored).
+            const uint4 *krow = reinterpret_cast<const uint4 *>(sl + ac * 256);
+            const uint4 *qrow = reinterpret_cast<const uint4 *>(qkv_l + min(ac, R - 1) * D);
+            uint4 kv[D / 32], qv[D / 32];
+#pragma unroll
+            for (int u = 0; u < D / 32; ++u) {
+                kv[u] = krow[(4 * u + ag - ac) & 15];
+                qv[u] = qrow[4 * u + ag];
+            }
+            if (has_new) {
+                const uint4 *knew = reinterpret_cast<const uint4 *>(qkv_l + RMAX * D);
+#pragma unroll
+                for (int u = 0; u < D / 32; ++u) {
+                    const uint4 kn = knew[4 * u + ag];
+                    if (ac == newk) kv[u] = kn;
+                }
+            }
+            f4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < D / 32; ++u)
+                st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[u]), as_bf16x8(qv[u]), st, 0, 0, 0);
+            // lane (ac = head, ag): keys 4 ag + r; keys 0-3 in lanes 0-15, 4-7 in lanes 16-31
+            float sv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sv[r] = (4 * ag + r < nval) ? st[r] * a.scale_log2 : -INFINITY;
+            float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            float x0, x1;
+            swap16(bm, x0, x1);
+            bm = fmaxf(x0, x1);                                // rows 0, 1: the max over the 8 keys
+            float pv[4], ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pv[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - bm);
+                ps += pv[r];
+            }
+            swap16(ps, x0, x1);
+            ps = x0 + x1;
+            // operand B of O^T: lane (head ac, k group 0) holds keys 0..7 as bf16, the
+            // other k groups zero
+            float pk[8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) swap16(pv[r], pk[r], pk[4 + r]);
+            uint4 pw = make_uint4(cvt_pk_bf16(pk[0], pk[1]), cvt_pk_bf16(pk[2], pk[3]), cvt_pk_bf16(pk[4], pk[5]),
+                                  cvt_pk_bf16(pk[6], pk[7]));
+            if (ag != 0) pw = make_uint4(0u, 0u, 0u, 0u);
+            const bf16x8_t pb8 = as_bf16x8(pw);
+            // operand A of O^T: V^T row (dim 16 n + ac) over keys 0..7 for k group 0, zero
+            // for the others (their B is zero, and a zero A keeps them finite).  Block
+            // with the new key: its value comes from LDS; keys past the range are zeroed
+            // (their p is 0; cache slots past the length may hold anything).
+            const uint4 *vrow = reinterpret_cast<const uint4 *>(sl + 2048 + ac * 16);
+            const bool live = ag == 0;
+            if (!has_new && nval == 8) {
+#pragma unroll
+                for (int n = 0; n < D / 16; ++n) {
+                    uint4 vv = vrow[16 * n];
+                    if (!live) vv = make_uint4(0u, 0u, 0u, 0u);
+                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), pb8, f4{0.f, 0.f, 0.f, 0.f},
+                                                                         0, 0, 0);
+                    // lane (head ac, ag): dims 16 n + 4 ag + r
+                    if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
+                }
             } else {
-                const uint4 *kr = reinterpret_cast<const uint4 *>(sl + akey * 256);
-                k0 = kr[(2 * asg - akey) & 15];
-                k1 = kr[(2 * asg + 1 - akey) & 15];
-            }
-            float sc[RMAX];
+                uint32_t km[4];                                // per word: its elements < nval
 #pragma unroll
-            for (int r = 0; r < RMAX; ++r) {
-                if (r < R) {
-                    const uint4 *qp = reinterpret_cast<const uint4 *>(qkv_l + r * D) + 2 * asg;
-                    const uint4 q0 = qp[0], q1 = qp[1];
-                    float d = 0.f;
+                for (int w = 0; w < 4; ++w)
+                    km[w] = nval >= 2 * w + 2 ? 0xFFFFFFFFu : nval == 2 * w + 1 ? 0x0000FFFFu : 0u;
+                uint32_t nm[4];                                // per word: the new key's half
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(bfe(q0, e), bfe(k0, e), d);
+                for (int w = 0; w < 4; ++w) nm[w] = (has_new && (newk >> 1) == w) ? (0xFFFFu << ((newk & 1) * 16)) : 0u;
+                const int nsh = (newk & 1) * 16;
+                const uint16_t *vnew = qkv_l + RMAX * D + D + ac;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) d = fmaf(bfe(q1, e), bfe(k1, e), d);
-                    d = group8_sum(d);
-                    sc[r] = kvalid ? d * a.scale_log2 : -INFINITY;
-                } else {
-                    sc[r] = -INFINITY;
+                for (int n = 0; n < D / 16; ++n) {
+                    uint4 vv = vrow[16 * n];
+                    const uint32_t nv = (uint32_t)vnew[16 * n] << nsh;
+                    vv.x = ((vv.x & ~nm[0]) | (nv & nm[0])) & km[0];
+                    vv.y = ((vv.y & ~nm[1]) | (nv & nm[1])) & km[1];
+                    vv.z = ((vv.z & ~nm[2]) | (nv & nm[2])) & km[2];
+                    vv.w = ((vv.w & ~nm[3]) | (nv & nm[3])) & km[3];
+                    if (!live) vv = make_uint4(0u, 0u, 0u, 0u);
+                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), pb8, f4{0.f, 0.f, 0.f, 0.f},
+                                                                         0, 0, 0);
+                    if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
                 }
             }
-            float p[RMAX];
-#pragma unroll
-            for (int r = 0; r < RMAX; ++r) {
-                const float bm = groups_max(sc[r]);
-                p[r] = (sc[r] == -INFINITY) ? 0.f : exp2f(sc[r] - bm);
-                al[r] = groups_sum(p[r]);
-                am[r] = bm;
-                ao[r][0] = 0.f;
-                ao[r][1] = 0.f;
-            }
-            // O += P V over the valid keys of the block; lane dims lane and lane + 64 (V^T rows
-            // of 16 B: 16 lanes read 256 contiguous bytes)
-            const uint4 va = *reinterpret_cast<const uint4 *>(sl + 2048 + lane * 16);
-            const uint4 vb = *reinterpret_cast<const uint4 *>(sl + 2048 + (lane + 64) * 16);
-            const uint32_t vn0 = qkv_l[RMAX * D + D + lane], vn1 = qkv_l[RMAX * D + D + lane + 64];
-            const int nval = min(8, au.hi - kb);               // wave-uniform
-#pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                if (kk < nval) {
-                    float fa = bfe(va, kk), fb = bfe(vb, kk);
-                    if (kk == newk) {
-                        fa = __uint_as_float(vn0 << 16);
-                        fb = __uint_as_float(vn1 << 16);
-                    }
-#pragma unroll
-                    for (int r = 0; r < RMAX; ++r) {
-                        const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[r]), 8 * kk));
-                        ao[r][0] = fmaf(pk, fa, ao[r][0]);
-                        ao[r][1] = fmaf(pk, fb, ao[r][1]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < RMAX; ++r) {
-                if (lane == 0) {
-                    stw[r * (D + 2) + D] = am[r];
-                    stw[r * (D + 2) + D + 1] = al[r];
-                }
-                stw[r * (D + 2) + lane] = ao[r][0];
-                stw[r * (D + 2) + lane + 64] = ao[r][1];
+            if (ac < R && ag == 0) {
+                stw[ac * (D + 4) + D] = bm;
+                stw[ac * (D + 4) + D + 1] = ps;
             }
         };
 
@@ -950,7 +971,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         int staged = 0;
         auto catch_up = [&](int k) __attribute__((always_inline)) {
             while (staged <= k) {
-                boundary(staged);
+                boundary(staged, std::false_type{});
                 ++staged;
             }
         };
@@ -1090,12 +1111,16 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     size_t off = (size_t)WORKERS * TRING * SLOT;
     // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 2) floats
     const int kps_max = ((m->T_cap + NR - 1) / NR + 7) & ~7;
-    const size_t ast_bytes = (size_t)(kps_max / 8) * RMAX * (D + 2) * 4;
+    const int n_items = kps_max / 8;
+    a.n_items = n_items;
+    const size_t ast_bytes = (size_t)n_items * RMAX * (D + 4) * 4;
     a.o_xl = (int)off; off += align16(std::max((size_t)Kmax * 2, ast_bytes));
     a.o_xzero = (int)off; off += 1024;
     a.o_xs = (int)off; off += align16((size_t)(Kmax / 64) * 4);
     // projection partials, or the attention merge [RMAX][D + 2]
-    a.o_part = (int)off; off += align16(std::max((size_t)max_items * 64, (size_t)RMAX * (D + 2) * 4));
+    // (attention: the merge [RMAX][D + 2], its weights [RMAX][n_items] and maxima [RMAX])
+    a.o_part = (int)off;
+    off += align16(std::max((size_t)max_items * 64, ((size_t)RMAX * (D + 2) + (size_t)RMAX * n_items + RMAX) * 4));
     a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
     a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
     a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
@@ -1129,6 +1154,10 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     SC_HIP_CHECK(hipMemcpy(mb, &one, 4, hipMemcpyHostToDevice));   // epoch base starts at 1
     a.layers = pl->d_layers;
     for (int i = 0; i < B_COUNT; ++i) a.buf[i] = reinterpret_cast<uint2 *>(mb + boff[i]);
+    for (int i = 0; i < 4; ++i) {
+        a.gd[i].in = a.buf[a.gd[i].in_buf];
+        a.gd[i].out = a.buf[a.gd[i].out_buf];
+    }
     a.counters = m->counters;
     a.epoch_base = reinterpret_cast<uint32_t *>(mb);
     a.status = reinterpret_cast<unsigned *>(mb + 64);

@@ -155,9 +155,7 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
     auto put_x = [&](int c, uint4 v) {
         xl[c] = BITS == 4 ? perm_w4x(v) : v;
         float g = sum_bf16x8(v);                        // the 8 chunks of a group sit in 8 adjacent lanes
-        g += __shfl_xor(g, 1);
-        g += __shfl_xor(g, 2);
-        g += __shfl_xor(g, 4);
+        g = group8_sum(g);
         if ((c & 7) == 0) xs[c >> 3] = g;
     };
     if (PRO == M1_PRO_NORM) {
@@ -259,7 +257,7 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
             const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
             acc = fmaf(sf, P4[t][0], fmaf(cf, xsv[t], acc));
         }
-        if (BITS == 4) acc += __shfl_xor(acc, 32);     // D row 0 (lanes 0-15) + D row 8 (lanes 32-47)
+        if (BITS == 4) acc = xor32_sum(acc);           // D row 0 (lanes 0-15) + D row 8 (lanes 32-47)
         if (q == 0) part[item * 16 + j] = acc;
     };
     auto claim = [&]() -> int {

@@ -59,11 +59,63 @@ __device__ __forceinline__ float bfe(uint4 v, int e) {
     return (e & 1) ? __uint_as_float(w & 0xFFFF0000u) : __uint_as_float(w << 16);
 }
 
-// xor-tree sum over the 64 lanes (every lane gets the same total)
+// ---------------------------------------------------------------- lane exchanges
+//
+// Butterfly partners on the VALU: DPP moves inside rows of 16 lanes and the gfx950
+// permlane swaps across rows, instead of LDS-routed shuffles.  A butterfly step
+// v_l + v_(l xor d) gives every lane of a pair the same bits (one rounding of a
+// commutative sum), so these reproduce the __shfl_xor trees exactly.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1;          // quad_perm [1, 0, 3, 2]: lane l <- l ^ 1
+constexpr int DPP_XOR2 = 0x4E;          // quad_perm [2, 3, 0, 1]: lane l <- l ^ 2
+constexpr int DPP_XOR3 = 0x1B;          // quad_perm [3, 2, 1, 0]: lane l <- l ^ 3
+constexpr int DPP_HALF_MIRROR = 0x141;  // lane l <- l ^ 7 (within 8)
+constexpr int DPP_ROR8 = 0x128;         // lane l <- l ^ 8 (within 16)
+
+// rows of 16 lanes (r0 r1 r2 r3) -> a = (r0 r0 r2 r2), b = (r1 r1 r3 r3)
+__device__ __forceinline__ void swap16(float v, float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+// halves (lo hi) -> a = (lo lo), b = (hi hi)
+__device__ __forceinline__ void swap32(float v, float &a, float &b) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+// v + v of lane l ^ 32
+__device__ __forceinline__ float xor32_sum(float v) {
+    float a, b;
+    swap32(v, a, b);
+    return a + b;
+}
+// v of lane l ^ 4
+__device__ __forceinline__ float xor4_mov(float v) { return dpp_mov<DPP_HALF_MIRROR>(dpp_mov<DPP_XOR3>(v)); }
+
+// sum over the 8 lanes 8g .. 8g + 7, as the tree over distances 1, 2, 4
+__device__ __forceinline__ float group8_sum(float v) {
+    v += dpp_mov<DPP_XOR1>(v);
+    v += dpp_mov<DPP_XOR2>(v);
+    return v + dpp_mov<DPP_HALF_MIRROR>(v);     // after the quad sums, lane l ^ 7 holds lane l ^ 4's value
+}
+
+// xor-tree sum over the 64 lanes, distances 32, 16, 8, 4, 2, 1 (every lane gets the
+// same total)
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    float a, b;
+    swap32(v, a, b);
+    v = a + b;
+    swap16(v, a, b);
+    v = a + b;
+    v += dpp_mov<DPP_ROR8>(v);
+    v += xor4_mov(v);
+    v += dpp_mov<DPP_XOR2>(v);
+    return v + dpp_mov<DPP_XOR1>(v);
 }
 
 // bf16(a + b), 8 packed bf16
