@@ -150,6 +150,28 @@ __device__ __forceinline__ float lanes_max(float v) {
     return groups_max(fmaxf(v, dpp_mov<DPP_HALF_MIRROR>(v)));
 }
 
+// Columns (p[16 ch], p[16 ch + 1]) summed over the tile's K chunks ch < cpt in chunk
+// order (qgemv_m1_kernel's order, so the bits match), the LDS reads issued 8 chunks
+// at a time.
+__device__ __forceinline__ void chunk_sums(const float *p, int cpt, float &s0, float &s1) {
+    int ch = 0;
+    for (; ch + 8 <= cpt; ch += 8) {
+        float2 t[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) t[k] = *reinterpret_cast<const float2 *>(p + (ch + k) * 16);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            s0 += t[k].x;
+            s1 += t[k].y;
+        }
+    }
+    for (; ch < cpt; ++ch) {
+        const float2 t = *reinterpret_cast<const float2 *>(p + ch * 16);
+        s0 += t.x;
+        s1 += t.y;
+    }
+}
+
 struct AttnUnit {
     int valid, kvh, r, lo, hi;   // keys [lo, hi) of kv head kvh (hi includes the new position)
 };
@@ -427,7 +449,15 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     for (int t = tid; t < a.R * ni; t += THREADS) {
                         const int h = t / ni, w = t - h * ni;
                         float M = -INFINITY;
-                        for (int v = 0; v < ni; ++v) M = fmaxf(M, ast[v * AST + h * (D + 4) + D]);
+                        int v = 0;
+                        for (; v + 4 <= ni; v += 4) {              // reads 4 at a time
+                            float t[4];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) t[k] = ast[(v + k) * AST + h * (D + 4) + D];
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) M = fmaxf(M, t[k]);
+                        }
+                        for (; v < ni; ++v) M = fmaxf(M, ast[v * AST + h * (D + 4) + D]);
                         const float mw = ast[w * AST + h * (D + 4) + D];
                         fac[h * ni + w] = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
                         if (w == 0) mh[h] = M;
@@ -440,7 +470,19 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             acc = ni > 0 ? mh[h] : -INFINITY;
                         } else {
                             const float *src = ast + h * (D + 4) + x;          // x = D + 1: l
-                            for (int w = 0; w < ni; ++w) acc = fmaf(fac[h * ni + w], src[w * AST], acc);
+                            const float *fh = fac + h * ni;
+                            int w = 0;
+                            for (; w + 4 <= ni; w += 4) {          // reads 4 items at a time
+                                float f[4], o[4];
+#pragma unroll
+                                for (int k = 0; k < 4; ++k) {
+                                    f[k] = fh[w + k];
+                                    o[k] = src[(w + k) * AST];
+                                }
+#pragma unroll
+                                for (int k = 0; k < 4; ++k) acc = fmaf(f[k], o[k], acc);
+                            }
+                            for (; w < ni; ++w) acc = fmaf(fh[w], src[w * AST], acc);
                         }
                         part[t] = acc;
                     }
@@ -473,12 +515,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             const int tl = wdx >> 2, c = 2 * (wdx & 3);
                             const float *pp = part + (size_t)tl * cpt * 16;
                             float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-                            for (int ch = 0; ch < cpt; ++ch) {
-                                g0 += pp[ch * 16 + c];
-                                g1 += pp[ch * 16 + c + 1];
-                                u0 += pp[ch * 16 + 8 + c];
-                                u1 += pp[ch * 16 + 8 + c + 1];
-                            }
+                            chunk_sums(pp + c, cpt, g0, g1);
+                            chunk_sums(pp + 8 + c, cpt, u0, u1);
                             const uint32_t o0 = f2bf(silu_mul_f(bf2f(f2bf(g0)), bf2f(f2bf(u0))));
                             const uint32_t o1 = f2bf(silu_mul_f(bf2f(f2bf(g1)), bf2f(f2bf(u1))));
                             ll_store(dst + ((tb + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
@@ -490,10 +528,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             const int tl = wdx >> 3, c = 2 * (wdx & 7);
                             const float *pp = part + (size_t)tl * cpt * 16;
                             float v0 = 0.f, v1 = 0.f;
-                            for (int ch = 0; ch < cpt; ++ch) {
-                                v0 += pp[ch * 16 + c];
-                                v1 += pp[ch * 16 + c + 1];
-                            }
+                            chunk_sums(pp + c, cpt, v0, v1);
                             const int n = (tb + tl) * 16 + c;
                             uint32_t o0 = f2bf(v0), o1 = f2bf(v1);
                             if (resid) {
