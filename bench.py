@@ -11,14 +11,22 @@ per token.  A "step" is one decode token for the whole batch.
 Printed (one JSON line on stdout):
 * ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
   bracketed by device synchronisation);
-* ``roofline``: the batch-1 decode qGEMV (``qgemv_m1_kernel<4, *, *>``, every
-  prologue/epilogue instantiation: plain, RMSNorm, RMSNorm + SwiGLU): algorithmic bytes
-  (packed weights + bf16 scales and biases + x + y) per launch, averaged over the
-  129 launches of one decode step, over the average launch duration: HIP events
-  on the replay stream around graph replays of exactly those launches (a graph
-  runs them back to back, so the average is the kernels' own), against 8 TB/s;
+* ``roofline``: the dominant kernel of a decode step.  At batch 1 that is the
+  whole-trunk launch ``decode_step_kernel<4>`` (embedding and every layer in one
+  persistent kernel; the step adds the final RMSNorm + lm_head GEMV and argmax):
+  algorithmic bytes per launch (every layer's packed weights + bf16 scales and
+  biases, the KV cache read at the step's length, the appended key/value, the
+  embedding row and the output row) over the average launch duration: HIP events
+  on the launch stream around back-to-back launches, against 8 TB/s.  Without the
+  trunk plan (batch > 1) it is the decode qGEMV, as ``qgemv_roofline``.
   ``traffic`` is the measured HBM bytes per launch recorded under ``profiles/``
   (null when absent);
+* ``qgemv_roofline``: the per-op batch-1 decode qGEMV (``qgemv_m1_kernel<4, *, *>``,
+  every prologue/epilogue instantiation: plain, RMSNorm, RMSNorm + SwiGLU) on the
+  same weights: algorithmic bytes (packed weights + bf16 scales and biases + x + y)
+  per launch, averaged over the 129 launches of one decode step, over the average
+  launch duration (HIP events on the replay stream around graph replays of exactly
+  those launches, so the average is the kernels' own), against 8 TB/s;
 * ``cpu_baseline``: the C restatement of the quantized matmul (OpenMP, fp64
   accumulation) timed on this host on a bounded sample: decoder layer 0's four
   projections plus 1/32 of the lm_head rows at M = batch, repeated for ~10 s,
@@ -41,6 +49,7 @@ METRIC = "W4 decode tok/s (Llama-3-8B shape, bs1) + qGEMV HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK = 2.5e15
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_m1_w4_llama3_8b_decode_traffic.json")
+TRUNK_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_step_w4_llama3_8b_traffic.json")
 
 LLAMA3_8B = dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv_heads=8, theta=500000.0, eps=1e-5)
 
@@ -63,6 +72,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernels-only", action="store_true",
                    help="build the weights and run only the per-launch GEMV pass (for counter profiling)")
+    p.add_argument("--trunk-only", action="store_true",
+                   help="prefill, then only eager whole-trunk decode launches (for counter profiling)")
     return p.parse_args()
 
 
@@ -279,6 +290,40 @@ def time_prefill_gemms(model, M, bits, reps):
             "per_shape": out}
 
 
+def trunk_bytes(model, cache_len, bits):
+    """Algorithmic bytes of one whole-trunk decode launch at batch 1 with ``cache_len``
+    positions cached: every layer's q|k|v, o, gate|up and down packed weights + bf16
+    scales and biases, the keys and values of cache_len + 1 positions read, the new
+    key and value written, the embedding row read and the output row written."""
+    att, mlp = model.layers[0].attention, model.layers[0].mlp
+    H, I = model.hidden_size, mlp.local_intermediate
+    D, Hkv = att.head_dim, att.local_num_kv_heads
+    qkvN = (att.local_num_heads + 2 * Hkv) * D
+    w = sum(N * K * bits // 8 + N * (K // 64) * 4
+            for N, K in ((qkvN, H), (H, att.local_num_heads * D), (2 * I, H), (H, I)))
+    kv = 2 * Hkv * (cache_len + 1) * D * 2 + 2 * Hkv * D * 2
+    return len(model.layers) * (w + kv) + 2 * H * 2
+
+
+def time_trunk_launches(dec, reps):
+    """Average duration of the whole-trunk launch: HIP events on the launch stream
+    around ``reps`` back-to-back eager launches of the plan (each recomputes the same
+    step: the cache slot and token id come from the counters it does not advance)."""
+    import torch
+    plan = dec.bufs.plan
+    plan.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        plan.run()
+    e1.record()
+    torch.cuda.synchronize()
+    if plan.status() != 0:
+        raise RuntimeError(f"trunk launch gave up (status {plan.status()})")
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
 def eager_gemv_passes(model, batch, bits, passes):
     """The same launches, eager (for hardware-counter runs, one dispatch at a time)."""
     import torch
@@ -386,6 +431,21 @@ def main():
 
     tokens = torch.zeros((B, W + K + 2), dtype=torch.int32, device="cuda")
     dec = DecodeGraph(model, cache, tokens)
+    if args.trunk_only:
+        if dec.bufs.plan is None:
+            log("trunk-only: the whole-trunk plan does not apply to this configuration")
+            sys.exit(2)
+        # a plain copy of known size first (256 MiB read + 256 MiB written), to scale
+        # the HBM counters, then eager trunk launches
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        us = time_trunk_launches(dec, args.kernel_reps)
+        log(f"trunk-only: 3 copies of {src.numel()} bytes, {args.kernel_reps + 1} trunk launches, "
+            f"{us:.1f} us each, {trunk_bytes(model, cache.length, args.bits)} bytes algorithmic per launch")
+        return
     _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
     _lib.add_i32(cache.counters[1:], 1, n=1)
     dec.run(1)            # eager step, then capture
@@ -400,20 +460,36 @@ def main():
     log(f"decode: {K} steps in {el * 1e3:.1f} ms -> {ms_step:.3f} ms/step, {tok_s:.1f} tok/s")
     first = tokens[0, :8].tolist()
 
+    trunk = None
+    if dec.bufs.plan is not None:
+        t_us = time_trunk_launches(dec, args.kernel_reps)
+        t_bytes = trunk_bytes(model, cache.length, args.bits)
+        trunk = dict(avg_us=t_us, bytes=t_bytes, GBs=t_bytes / (t_us * 1e-6) / 1e9)
+        log(f"trunk: {t_us:.1f} us/launch, {t_bytes / 1e9:.3f} GB/launch, {trunk['GBs']:.0f} GB/s")
     g = time_gemv_launches(model, B, args.bits, args.kernel_reps)
     gemm = time_prefill_gemms(model, P * B, args.bits, args.kernel_reps) if P * B >= 128 else None
     step_gemv_bytes = g["bytes_per_launch"] * g["launches_per_step"]
     step_gemv_ms = g["avg_us"] * g["launches_per_step"] / 1e3
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-    roof = {"bound": "hbm", "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": (f"qgemv_m1_kernel<{args.bits}, *, *>" if B == 1 else f"qgemv_dma_kernel<{args.bits}, 8, *, *>")
-                      if B <= 8 else "qgemv",
-            "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
-            "launches_per_step": g["launches_per_step"]}
+    def traffic_of(path):
+        if os.path.exists(path):
+            with open(path) as f:
+                return json.load(f).get("hbm_bytes_per_launch")
+        return None
+
+    qroof = {"bound": "hbm", "achieved": round(g["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+             "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "traffic": traffic_of(TRAFFIC_FILE),
+             "kernel": (f"qgemv_m1_kernel<{args.bits}, *, *>" if B == 1 else f"qgemv_dma_kernel<{args.bits}, 8, *, *>")
+                       if B <= 8 else "qgemv",
+             "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
+             "launches_per_step": g["launches_per_step"]}
+    if trunk is not None:
+        roof = {"bound": "hbm", "achieved": round(trunk["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(trunk["GBs"] / HBM_PEAK_GBS, 4),
+                "traffic": traffic_of(TRUNK_TRAFFIC_FILE) if args.bits == 4 and args.layers == 32 else None,
+                "kernel": f"decode_step_kernel<{args.bits}>", "avg_launch_us": round(trunk["avg_us"], 2),
+                "bytes_per_launch": int(trunk["bytes"]), "launches_per_step": 1}
+    else:
+        roof = qroof
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -434,10 +510,12 @@ def main():
                    "kv_heads": cfg["kv_heads"], "vocab": cfg["vocab"], "weights": f"W{args.bits} g64, bf16 s/b",
                    "activations": "bf16, fp32 accumulate", "decode": "HIP graph replay per token"},
         "roofline": roof,
+        "qgemv_roofline": qroof,
         "cpu_baseline": cpu,
         "prefill": {"tokens": B * P, "ms": round(prefill_s * 1e3, 2), "tok_s": round(B * P / prefill_s, 1),
                     "qgemm_roofline": gemm},
-        "decode_step": {"gemv_ms": round(step_gemv_ms, 4), "gemv_bytes": int(step_gemv_bytes),
+        "decode_step": {"path": "whole-trunk launch + lm_head GEMV + argmax" if trunk is not None
+                        else "per-op launches", "gemv_ms": round(step_gemv_ms, 4), "gemv_bytes": int(step_gemv_bytes),
                         "kv_bytes_avg": int(kv_bytes),
                         "step_hbm_frac": round((step_gemv_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9
                                                / HBM_PEAK_GBS, 4)},

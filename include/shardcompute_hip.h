@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 5
+#define SC_ABI_VERSION 6
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -271,8 +271,10 @@ int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream);
  * the final RMSNorm + lm_head read, and every layer's cache holds the new position.
  *
  * sc_decode_plan_create validates the shapes (head_dim 128, at most 4 query heads per
- * kv head, widths multiples of 512, group size 64), uploads the op list and
- * allocates the plan's exchange buffers (a few MB); sc_decode_plan_run enqueues the
+ * kv head, widths multiples of 512 up to 16384, group size 64, the attention rows and
+ * key ranges splitting over the device's CUs, the whole working set within one CU's
+ * LDS), uploads the per-layer pointer table and allocates the plan's exchange buffers
+ * (a few MB; -2 for a shape it does not take); sc_decode_plan_run enqueues the
  * launch on `hip_stream` (capturable: it allocates nothing and calls no memset).
  * Launches of one plan must not overlap.  sc_decode_plan_status copies the plan's
  * status word (0: every launch completed; nonzero: a launch gave up after a bounded

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
