@@ -695,14 +695,29 @@ argmax_kernel(const uint16_t *__restrict__ logits, long V, int32_t *__restrict__
     unsigned long long best = 0;
     const bool vec = ((V & 7) == 0);
     if (vec) {
+        // 16 loads per thread in flight before any is reduced (a row's logits are
+        // read in one memory round trip rather than one per loop pass)
+        constexpr int U = 16;
         const uint4 *lv = reinterpret_cast<const uint4 *>(lr);
-        for (long i = threadIdx.x; i < V / 8; i += blockDim.x) {
-            const uint4 v = lv[i];
+        const long n8 = V / 8;
+        for (long i0 = threadIdx.x; i0 < n8; i0 += (long)U * blockDim.x) {
+            uint4 v[U];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t w = e < 2 ? v.x : e < 4 ? v.y : e < 6 ? v.z : v.w;
-                const unsigned long long kk = argmax_key((e & 1) ? (w >> 16) : w, (uint32_t)(8 * i + e));
-                best = kk > best ? kk : best;
+            for (int u = 0; u < U; ++u) {
+                const long i = i0 + (long)u * blockDim.x;
+                v[u] = i < n8 ? lv[i] : make_uint4(0u, 0u, 0u, 0u);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long i = i0 + (long)u * blockDim.x;
+                if (i < n8) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t w = e < 2 ? v[u].x : e < 4 ? v[u].y : e < 6 ? v[u].z : v[u].w;
+                        const unsigned long long kk = argmax_key((e & 1) ? (w >> 16) : w, (uint32_t)(8 * i + e));
+                        best = kk > best ? kk : best;
+                    }
+                }
             }
         }
     } else {

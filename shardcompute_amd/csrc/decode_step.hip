@@ -75,6 +75,7 @@ struct GemvDesc {
     int flags, in_buf, out_buf;
     const uint2 *in;        // LL words of the input and the output (exchange buffers in_buf, out_buf)
     uint2 *out;
+    int tb, ntl;            // this workgroup's tiles [tb, tb + ntl) (set in LDS at launch)
 };
 
 // Device pointers of one layer: projections q|k|v, o, gate|up, down; norms; cache.
@@ -241,7 +242,10 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             for (int c = lane; c < n; c += 64) dst[c] = src[c];
         }
         if (lane < 4) {
-            const GemvDesc g = lane == 0 ? a.gd[0] : lane == 1 ? a.gd[1] : lane == 2 ? a.gd[2] : a.gd[3];
+            GemvDesc g = lane == 0 ? a.gd[0] : lane == 1 ? a.gd[1] : lane == 2 ? a.gd[2] : a.gd[3];
+            int te;
+            gemv_tiles(g.T, wg, P, g.tb, te);
+            g.ntl = te - g.tb;
             sgd[lane] = g;
         }
         if (lane == 0) {
@@ -293,9 +297,9 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
 
     // Control wave: gather n8 chunks of 8 bf16 (chunk c = LL words [addr(c), +4)) that
     // carry epoch ep; put(c, v) receives each chunk once (per lane; no cross-lane
-    // operations inside).  Batches of 4 chunks per lane; the first pass keeps two
-    // batches in flight (one round trip for inputs that are already published), later
-    // passes re-read the batches still missing a chunk.
+    // operations inside).  Batches of 4 chunks per lane, two batches in flight (one
+    // round trip for inputs that are already published); later passes re-read the
+    // batches still missing a chunk.
     auto ll_gather = [&](auto addr, int n8, uint32_t ep, auto put) __attribute__((always_inline)) -> bool {
         constexpr int CPL = 4;                           // chunks per lane per batch
         constexpr int BCH = 64 * CPL;                    // chunks per batch
@@ -337,11 +341,17 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             if (bi + 2 < nb) load(bi + 2, va);
             if (bi + 1 < nb) check(bi + 1, vb);
         }
+        // later passes: the batches still missing a chunk, two at a time (one round trip
+        // per pair)
         for (int it = 0; __ballot(pend != 0u) != 0ull; ++it) {
-            for (int bi = 0; bi < nb; ++bi) {
-                if (__ballot(((pend >> (CPL * bi)) & ((1u << CPL) - 1u)) != 0u) == 0ull) continue;
-                load(bi, va);
-                check(bi, va);
+            for (int bi = 0; bi < nb; bi += 2) {
+                const bool p0 = __ballot(((pend >> (CPL * bi)) & ((1u << CPL) - 1u)) != 0u) != 0ull;
+                const bool p1 =
+                    bi + 1 < nb && __ballot(((pend >> (CPL * (bi + 1))) & ((1u << CPL) - 1u)) != 0u) != 0ull;
+                if (p0) load(bi, va);
+                if (p1) load(bi + 1, vb);
+                if (p0) check(bi, va);
+                if (p1) check(bi + 1, vb);
             }
             if ((it & 15) == 15 && (timed_out() ||
                 __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
@@ -504,9 +514,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                         ll_store(a.buf[B_H] + w, inr ? row[w] : 0u, ep);
                 } else {
                     const GemvDesc &o = sgd[gemv_index(kp)];
-                    int tb, te;
-                    gemv_tiles(o.T, wg, P, tb, te);
-                    const int ntl = te - tb, cpt = o.cpt;
+                    const int tb = o.tb, ntl = o.ntl, cpt = o.cpt;
                     uint2 *dst = o.out;
                     uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
                     if (o.flags & F_SWIGLU) {
