@@ -141,12 +141,15 @@ __device__ __forceinline__ float rms_root(float tot, int D, float eps) {
     return __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)D), eps));
 }
 
-// bf16((h / root) * w): divide by the root, then scale (transformer.py:55)
+// bf16((h / root) * w): divide by the root, then scale (transformer.py:55).  Every
+// kernel that normalises (standalone, the GEMV prologues, the decode trunk) uses this,
+// so they agree bit for bit; the rounding is RNE in one instruction per pair (a NaN
+// input stays NaN, its payload may differ from f2bf's)
 __device__ __forceinline__ uint4 norm_bf16x8(uint4 h, uint4 w, float root) {
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        o[e] = pack_bf16x2(mul_rn(__fdiv_rn(bfe(h, 2 * e), root), bfe(w, 2 * e)),
+        o[e] = cvt_pk_bf16(mul_rn(__fdiv_rn(bfe(h, 2 * e), root), bfe(w, 2 * e)),
                            mul_rn(__fdiv_rn(bfe(h, 2 * e + 1), root), bfe(w, 2 * e + 1)));
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
