@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 6
+#define SC_ABI_VERSION 7
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -126,6 +126,33 @@ int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
                         uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
                         const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N,
                         int64_t K, int bits, int group_size, void *hip_stream);
+
+/* Bytes of the sc_decode_head_bf16 workspace. */
+#define SC_DECODE_HEAD_WORKSPACE_BYTES 16
+
+/*
+ * The greedy tail of a decode step: logits = qmm(RMSNorm(x + residual)) exactly
+ * as sc_qmm_rmsnorm_bf16 (same arguments, logits [M, N] in place of y), then
+ * ids / tokens exactly as sc_argmax_bf16 on the logits, then counters[i] += 1 for
+ * i < n_counters as sc_add_i32 (step_or_null may point into the counters: the
+ * token column is read before they advance).  At M = 1 the decode GEMV selects the
+ * token while it writes the logits (its workgroups max their outputs' keys into
+ * the workspace; the last to finish writes the token and advances the counters),
+ * so no second pass over the logits runs; otherwise the three steps run in turn.
+ * workspace: SC_DECODE_HEAD_WORKSPACE_BYTES, 16-byte aligned, zero before the
+ * first call; every call leaves it zero.  Calls that share a workspace must not
+ * overlap (one stream).  Replaces the final norm and lm_head of the decode step
+ * (src/shardcompute/parallel/transformer.py:562, :575) with the greedy mx.argmax of
+ * src/shardcompute/worker/executor.py:276-278 and the cache-length bookkeeping of
+ * executor.py:134-136.
+ */
+int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,
+                        uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
+                        const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *logits, int64_t M, int64_t N,
+                        int64_t K, int bits, int group_size, int32_t *ids, int32_t *tokens_or_null,
+                        int64_t tokens_stride, int64_t tokens_cols, const int32_t *step_or_null,
+                        int32_t *counters_or_null, int64_t n_counters, void *workspace, int64_t workspace_bytes,
+                        void *hip_stream);
 
 /*
  * act = silu(gate) * up for the stacked gate|up weight wq [2I, K*bits/32] (gate rows

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -28,6 +28,7 @@ EXPORTS = (
     "sc_dequantize_bf16",
     "sc_quantize_affine",
     "sc_qmm_rmsnorm_bf16",
+    "sc_decode_head_bf16",
     "sc_qmm_swiglu_bf16",
     "sc_rms_norm_bf16",
     "sc_rope_append_kv_bf16",
@@ -86,6 +87,9 @@ def load():
         f32 = ctypes.c_float
         lib.sc_qmm_rmsnorm_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
         lib.sc_qmm_rmsnorm_bf16.restype = i32
+        lib.sc_decode_head_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p, p, i64,
+                                            i64, p, p, i64, p, i64, p]
+        lib.sc_decode_head_bf16.restype = i32
         lib.sc_qmm_swiglu_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
         lib.sc_qmm_swiglu_bf16.restype = i32
         lib.sc_rms_norm_bf16.argtypes = [p, p, p, p, p, i64, i64, f32, p]
@@ -247,6 +251,56 @@ def qmm_rmsnorm(x, norm_weight, eps, wq, scales, biases, residual=None, h_out=No
                                  _ptr(xn), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y), M, N, K, bits,
                                  group_size, _stream(x))
     _check(rc, "sc_qmm_rmsnorm_bf16")
+    return y.reshape(*lead, N), xn.reshape(*lead, K)
+
+
+DECODE_HEAD_WORKSPACE_BYTES = 16
+
+
+def decode_head(x, norm_weight, eps, wq, scales, biases, ids, workspace, residual=None, h_out=None, xn_out=None,
+                bias=None, bits=4, group_size=64, out=None, tokens=None, step=None, counters=None, n_counters=0):
+    """The greedy tail of a decode step: logits = qmm(RMSNorm(x + residual)), then
+    ``ids`` (and ``tokens[:, step[0]]``) = the first-max index of each logits row,
+    then ``counters[:n_counters] += 1``.  ``workspace``: a zeroed device buffer of
+    at least DECODE_HEAD_WORKSPACE_BYTES, left zero by every call.  Returns
+    (logits, xn)."""
+    lib = load()
+    _require_gpu(x, norm_weight, wq, scales, biases, ids, workspace, residual, h_out, xn_out, bias, out, tokens,
+                 step, counters)
+    K = x.shape[-1]
+    _rows(x, K, "x")
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    wq, scales, biases, bias, N = _qmm_common(wq, scales, biases, bias, bits, group_size, K)
+    if residual is not None:
+        _rows(residual, K, "residual")
+    if h_out is not None:
+        _rows(h_out, K, "h_out")
+    if norm_weight.shape != (K,) or norm_weight.dtype != torch.bfloat16:
+        raise ValueError(f"norm weight must be bf16 [{K}]")
+    _i32(ids, "ids")
+    if ids.numel() != M or not ids.is_contiguous():
+        raise ValueError(f"ids must be a contiguous int32 buffer of {M} entries")
+    if workspace.nbytes < DECODE_HEAD_WORKSPACE_BYTES or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous buffer of at least {DECODE_HEAD_WORKSPACE_BYTES} bytes")
+    if tokens is not None:
+        _i32(tokens, "tokens")
+        if tokens.dim() != 2 or tokens.shape[0] != M or tokens.stride(1) != 1:
+            raise ValueError("tokens must be a row-major [rows, n] int32 matrix")
+    if n_counters:
+        _i32(counters, "counters")
+        if counters.numel() < n_counters or not counters.is_contiguous():
+            raise ValueError(f"counters must hold {n_counters} contiguous int32 entries")
+    xn = xn_out if xn_out is not None else torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
+    _rows(xn, K, "xn_out")
+    y = out if out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    rc = lib.sc_decode_head_bf16(_ptr(x), _ptr(residual), _ptr(norm_weight.contiguous()), float(eps), _ptr(h_out),
+                                 _ptr(xn), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y), M, N, K, bits,
+                                 group_size, _ptr(ids), _ptr(tokens), tokens.stride(0) if tokens is not None else 0,
+                                 tokens.shape[1] if tokens is not None else 0, _ptr(step),
+                                 _ptr(counters) if n_counters else None, int(n_counters), _ptr(workspace),
+                                 workspace.nbytes, _stream(x))
+    _check(rc, "sc_decode_head_bf16")
     return y.reshape(*lead, N), xn.reshape(*lead, K)
 
 

@@ -189,7 +189,8 @@ static bool overlap(const void *a, size_t an, const void *b, size_t bn) {
 static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw, float eps, uint16_t *h_out,
                      uint16_t *x_out, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
                      uint16_t *y, int64_t M, int64_t N, int64_t K, int bits, int group_size, void *stream,
-                     int64_t swiglu_half, uint16_t *gu_scratch) {
+                     int64_t swiglu_half, uint16_t *gu_scratch, const HeadArgmax *head = nullptr,
+                     bool *head_done = nullptr) {
     const char *what = swiglu_half ? "qmm_swiglu" : "qmm_rmsnorm";
     const uint16_t *xin = nw ? x_out : x;
     int rc = check_qmm(xin, wq, s, b, y, M, N, K, bits, group_size);
@@ -217,10 +218,21 @@ static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw,
                 return set_error(SC_EINVAL, "%s: output buffers overlap", what);
     }
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (head_done) *head_done = false;
     if (qgemv_dma_eligible(xin, wq, s, b, (int)M, (int)K)) {
-        DmaFused f{nw ? PRO_NORM_KIND : 0, (int)swiglu_half, res, nw, eps, res ? h_out : nullptr, x_out};
+        // with a greedy head the batch-1 kernel selects the token itself; where it
+        // does not apply the product runs alone and the caller selects
+        DmaFused f{nw ? PRO_NORM_KIND : 0, (int)swiglu_half, res, nw, eps, res ? h_out : nullptr, x_out, head};
         rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, &f);
-        if (rc != SC_EUNSUPPORTED) return rc;
+        if (rc != SC_EUNSUPPORTED) {
+            if (head_done) *head_done = head && rc == SC_OK;
+            return rc;
+        }
+        if (head) {
+            f.head = nullptr;
+            rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, &f);
+            if (rc != SC_EUNSUPPORTED) return rc;
+        }
     }
     if (nw) {
         rc = launch_rms_norm(x, res, nw, x_out, res ? h_out : nullptr, M, K, eps, st);
@@ -381,6 +393,36 @@ int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
     if (!norm_weight || !xn_out) return set_error(SC_EINVAL, "qmm_rmsnorm: null pointer argument");
     return qmm_fused(x, residual_or_null, norm_weight, eps, h_out_or_null, xn_out, wq, scales, biases, bias_or_null, y,
                      M, N, K, bits, group_size, hip_stream, 0, nullptr);
+}
+
+int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,
+                        uint16_t *h_out_or_null, uint16_t *xn_out, const uint32_t *wq, const uint16_t *scales,
+                        const uint16_t *biases, const uint16_t *bias_or_null, uint16_t *logits, int64_t M, int64_t N,
+                        int64_t K, int bits, int group_size, int32_t *ids, int32_t *tokens_or_null,
+                        int64_t tokens_stride, int64_t tokens_cols, const int32_t *step_or_null,
+                        int32_t *counters_or_null, int64_t n_counters, void *workspace, int64_t workspace_bytes,
+                        void *hip_stream) {
+    if (!norm_weight || !xn_out || !ids) return set_error(SC_EINVAL, "decode_head: null pointer argument");
+    if (n_counters < 0 || n_counters > 64 || (n_counters && !counters_or_null))
+        return set_error(SC_EINVAL, "decode_head: n_counters=%lld (at most 64, with a counter buffer)",
+                         (long long)n_counters);
+    if (!workspace || !aligned(workspace, 16) || workspace_bytes < SC_DECODE_HEAD_WORKSPACE_BYTES)
+        return set_error(SC_EINVAL, "decode_head: workspace of %d bytes, 16-byte aligned, required",
+                         SC_DECODE_HEAD_WORKSPACE_BYTES);
+    if (N < 1 || N > 0x7FFFFFFFLL) return set_error(SC_EINVAL, "decode_head: N=%lld", (long long)N);
+    if (tokens_or_null && (tokens_cols < 1 || tokens_stride < tokens_cols))
+        return set_error(SC_EINVAL, "decode_head: bad token buffer");
+    hipStream_t st = reinterpret_cast<hipStream_t>(hip_stream);
+    HeadArgmax hd{reinterpret_cast<unsigned long long *>(workspace),
+                  reinterpret_cast<unsigned *>(static_cast<uint8_t *>(workspace) + 8),
+                  ids, tokens_or_null, (long)tokens_cols, step_or_null, counters_or_null, (int)n_counters};
+    bool done = false;
+    int rc = qmm_fused(x, residual_or_null, norm_weight, eps, h_out_or_null, xn_out, wq, scales, biases, bias_or_null,
+                       logits, M, N, K, bits, group_size, hip_stream, 0, nullptr, M == 1 ? &hd : nullptr, &done);
+    if (rc || done) return rc;
+    rc = launch_argmax(logits, M, N, ids, tokens_or_null, tokens_stride, tokens_cols, step_or_null, st);
+    if (rc || !n_counters) return rc;
+    return launch_add_i32(counters_or_null, n_counters, 1, st);
 }
 
 int sc_qmm_swiglu_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight_or_null,

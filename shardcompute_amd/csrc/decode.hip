@@ -674,32 +674,28 @@ silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, lon
 //
 // First index of the maximum of each row (worker/executor.py:276-278 at
 // temperature 0, numpy/MLX argmax semantics): NaN counts as the maximum and
-// -0.0 equals +0.0.  Keys (order-preserving 16-bit image, ~index) packed in 64
-// bits so one max-reduction yields the largest value at the smallest index.
-__device__ __forceinline__ unsigned long long argmax_key(uint32_t u, uint32_t idx) {
-    u &= 0xFFFFu;
-    uint32_t k;
-    if ((u & 0x7FFFu) > 0x7F80u) k = 0xFFFFu;
-    else {
-        if (u == 0x8000u) u = 0;
-        k = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
-    }
-    return ((unsigned long long)k << 32) | (0xFFFFFFFFu - idx);
-}
-
+// -0.0 equals +0.0.  Keys (argmax_key: order-preserving 16-bit image, ~index)
+// packed in 64 bits so one max-reduction yields the largest value at the smallest
+// index.
 __global__ void __launch_bounds__(1024)
 argmax_kernel(const uint16_t *__restrict__ logits, long V, int32_t *__restrict__ ids,
               int32_t *__restrict__ tokens, long tok_stride, long tok_cols, const int32_t *__restrict__ step) {
     const int row = blockIdx.x;
     const uint16_t *lr = logits + (size_t)row * V;
     unsigned long long best = 0;
-    const bool vec = ((V & 7) == 0);
+    // vector path: 16-byte rows, and the in-thread sequence number (below 8 per
+    // uint4 times the uint4s per thread) fits 16 bits
+    const bool vec = ((V & 7) == 0) && (V / 8 + blockDim.x - 1) / blockDim.x <= 8192;
     if (vec) {
-        // 16 loads per thread in flight before any is reduced (a row's logits are
-        // read in one memory round trip rather than one per loop pass)
+        // 16 loads per thread in flight before any is reduced; within the thread a
+        // 32-bit key (order-preserving value << 16 | 0xFFFF - s, s = the element's
+        // sequence number in this thread, increasing with its index) so each element
+        // costs one max; the winner is widened to the 64-bit (value, index) key below
         constexpr int U = 16;
         const uint4 *lv = reinterpret_cast<const uint4 *>(lr);
         const long n8 = V / 8;
+        uint32_t bl = 0u;                                   // 0: no element (no real key is 0)
+        int seq = 0;
         for (long i0 = threadIdx.x; i0 < n8; i0 += (long)U * blockDim.x) {
             uint4 v[U];
 #pragma unroll
@@ -714,11 +710,18 @@ argmax_kernel(const uint16_t *__restrict__ logits, long V, int32_t *__restrict__
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const uint32_t w = e < 2 ? v[u].x : e < 4 ? v[u].y : e < 6 ? v[u].z : v[u].w;
-                        const unsigned long long kk = argmax_key((e & 1) ? (w >> 16) : w, (uint32_t)(8 * i + e));
-                        best = kk > best ? kk : best;
+                        const uint32_t key = (uint32_t)(argmax_key((e & 1) ? (w >> 16) : w, 0u) >> 32);
+                        const uint32_t kk = (key << 16) | (0xFFFFu - (uint32_t)(seq + 8 * u + e));
+                        bl = kk > bl ? kk : bl;
                     }
                 }
             }
+            seq += 8 * U;
+        }
+        if (bl != 0u) {
+            const uint32_t sq = 0xFFFFu - (bl & 0xFFFFu);
+            const uint32_t idx = 8u * ((uint32_t)threadIdx.x + (sq >> 3) * blockDim.x) + (sq & 7u);
+            best = ((unsigned long long)(bl >> 16) << 32) | (0xFFFFFFFFu - idx);
         }
     } else {
         for (long i = threadIdx.x; i < V; i += blockDim.x) {

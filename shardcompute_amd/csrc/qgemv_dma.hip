@@ -537,9 +537,11 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
                      const DmaFused *fused) {
     if (M < 1 || M > 8) return SC_EUNSUPPORTED;
+    const bool head = fused && fused->head;             // greedy selection: the batch-1 kernel only
+    if (head && M != 1) return SC_EUNSUPPORTED;
     if (M == 1) {       // batch 1: the dynamically balanced kernel (qgemv_m1.hip) when it applies
         const int rc = launch_qgemv_m1(x, wq, s, b, bias, y, N, K, bits, stream, fused);
-        if (rc != SC_EUNSUPPORTED) return rc;
+        if (rc != SC_EUNSUPPORTED || head) return rc;
     }
     if (K % 512) return SC_EUNSUPPORTED;                       // 16-byte aligned scale rows, whole items
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16) || ((uintptr_t)wq % 16)) return SC_EUNSUPPORTED;

@@ -39,6 +39,7 @@ struct M1Args {
     uint16_t *h_out;         // PRO_NORM with res: x + res, written by workgroup 0
     uint16_t *x_out;         // PRO_NORM: the normalised row, written by workgroup 0
     int half;                // EPI_SWIGLU: I (gate rows; output width)
+    HeadArgmax hd;           // EPI_NONE with hd.key: greedy selection over y
 };
 
 namespace {
@@ -55,6 +56,40 @@ __device__ __forceinline__ float sum_bf16x8(uint4 v) {
     return s;
 }
 
+// Greedy selection after the outputs are written (HeadArgmax), by every thread of
+// every workgroup: the workgroup's largest key is maxed into *key, then the
+// workgroup arrives on *done; the last to arrive turns the key into the token,
+// clears the workspace and advances the counters.  Nothing waits on another
+// workgroup.  Only the two workspace words are shared within the launch (the
+// outputs, ids, tokens and counters are read by later launches), so no cache
+// maintenance is needed: each workgroup's max has returned (it is performed at
+// the device-wide coherence point of atomics) before its arrival is issued, so the
+// arrival that returns P - 1 follows every max, and the exchange issued after it
+// reads their combined value.
+__device__ __forceinline__ void head_finish(const HeadArgmax &hd, unsigned long long best, unsigned long long *kred) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned long long other = __shfl_xor(best, o);
+        best = other > best ? other : best;
+    }
+    if (lane == 0) kred[wave] = best;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) best = kred[w] > best ? kred[w] : best;
+    const unsigned long long was = __hip_atomic_fetch_max(hd.key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("" ::"v"(was) : "memory");             // the max has returned before the arrival issues
+    const unsigned prev = __hip_atomic_fetch_add(hd.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev != gridDim.x - 1) return;
+    const unsigned long long k = __hip_atomic_exchange(hd.key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(hd.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int32_t id = (int32_t)(0xFFFFFFFFu - (uint32_t)k);
+    hd.ids[0] = id;
+    const long c = hd.step ? hd.step[0] : 0;            // read before the counters advance (step may be one)
+    if (hd.tokens && c >= 0 && c < hd.tok_cols) hd.tokens[c] = id;
+    for (int i = 0; i < hd.n_counters; ++i) hd.counters[i] += 1;
+}
+
 }  // namespace
 
 template <int BITS, int PRO, int EPI>
@@ -69,6 +104,7 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ int ctr;                                 // next item to claim
     __shared__ float red[NORM_THREADS / 64];
+    __shared__ unsigned long long kred[M1_MAX_WAVES];   // greedy selection: per-wave keys
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -309,6 +345,8 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
             a.y[col] = (uint16_t)f2bf(silu_mul_f(bf2f(gb), bf2f(ub)));
         }
     } else {
+        const bool head = a.hd.key != nullptr;
+        unsigned long long best = 0;
         for (int o = tid; o < ntl * 16; o += blockDim.x) {
             const int tl = o >> 4, c = o & 15;
             const int n = (t_begin + tl) * 16 + c;
@@ -319,7 +357,12 @@ __global__ void __launch_bounds__(64 * M1_MAX_WAVES) qgemv_m1_kernel(M1Args a) {
             uint32_t ob = f2bf(v);
             if (a.bias) ob = f2bf(bf2f(ob) + bf2f(a.bias[n]));
             a.y[n] = (uint16_t)ob;
+            if (head) {
+                const unsigned long long k = argmax_key(ob, (uint32_t)n);
+                best = k > best ? k : best;
+            }
         }
+        if (head) head_finish(a.hd, best, kred);
     }
 }
 
@@ -338,6 +381,8 @@ int launch_qgemv_m1(const uint16_t *x, const uint32_t *wq, const uint16_t *s, co
                                ((uintptr_t)fused->res % 16)))
         return SC_EUNSUPPORTED;
     if (half > 0 && (half % 8 || N != 2 * half)) return SC_EUNSUPPORTED;
+    const HeadArgmax *head = fused ? fused->head : nullptr;
+    if (head && (half > 0 || !head->key || !head->done || !head->ids)) return SC_EUNSUPPORTED;
     const DeviceInfo &di = device_info();
     const int item_k = bits == 4 ? 512 : 256;
     const int T = (N + 15) / 16;
@@ -346,7 +391,7 @@ int launch_qgemv_m1(const uint16_t *x, const uint32_t *wq, const uint16_t *s, co
     const int xunits = K / 512;
     const int stage_units = (pro == M1_PRO_NORM ? 3 : 1) * xunits;
     const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
-    const size_t static_lds = 64;                        // counter + norm partials
+    const size_t static_lds = 128;                       // counter + norm partials + per-wave keys
     int waves = 0, P = 0;
     size_t lds = 0;
     for (int w = M1_MAX_WAVES; w >= 4; w /= 2) {
@@ -373,6 +418,7 @@ int launch_qgemv_m1(const uint16_t *x, const uint32_t *wq, const uint16_t *s, co
     a.h_out = fused ? fused->h_out : nullptr;
     a.x_out = fused ? fused->x_out : nullptr;
     a.half = half;
+    a.hd = head ? *head : HeadArgmax{};
     auto launch = [&](auto kern, int &configured) -> int {
         if (lds > 65536 && (int)lds > configured) {
             SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),

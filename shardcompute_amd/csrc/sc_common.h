@@ -235,6 +235,35 @@ struct SplitKScratch {
 };
 int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out);
 
+// Arg-max key of a bf16 value: the order-preserving 16-bit image of the value
+// (NaN above +inf, -0.0 equal to +0.0) over ~index, so the larger key is the larger
+// value and, among equal values, the smaller index.  No key is 0.
+__device__ __forceinline__ unsigned long long argmax_key(uint32_t u, uint32_t idx) {
+    u &= 0xFFFFu;
+    uint32_t k;
+    if ((u & 0x7FFFu) > 0x7F80u) k = 0xFFFFu;
+    else {
+        if (u == 0x8000u) u = 0;
+        k = (u & 0x8000u) ? (~u & 0xFFFFu) : (u | 0x8000u);
+    }
+    return ((unsigned long long)k << 32) | (0xFFFFFFFFu - idx);
+}
+
+// Greedy token selection folded into a batch-1 GEMV's epilogue: every workgroup
+// maxes the keys of its outputs into *key; the last one to finish (counted in
+// *done) writes ids[0] and tokens[step[0]] (when 0 <= step[0] < tok_cols), adds 1
+// to counters[0, n_counters), and leaves *key and *done zero for the next call.
+struct HeadArgmax {
+    unsigned long long *key;
+    unsigned *done;
+    int32_t *ids;
+    int32_t *tokens;
+    long tok_cols;
+    const int32_t *step;
+    int32_t *counters;
+    int n_counters;
+};
+
 // Input transformation a decode GEMV can apply while staging its rows (see
 // qgemv_dma.hip): 1 = RMSNorm of x (+ res), 2 = silu(gate) * up of x = gate|up.
 struct DmaFused {
@@ -245,6 +274,7 @@ struct DmaFused {
     float eps;
     uint16_t *h_out;
     uint16_t *x_out;
+    const HeadArgmax *head = nullptr;   // batch-1 plain-output GEMV only
 };
 
 }  // namespace sc

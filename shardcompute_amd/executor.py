@@ -79,10 +79,14 @@ TokenCallback = Callable[[int, int, bool], Any]
 
 
 class DecodeGraph:
-    """One greedy decode step of ``model`` for ``batch`` sequences, as a replayable graph."""
+    """Greedy decode steps of ``model`` for ``batch`` sequences, as replayable graphs:
+    one of a single step and one of ``steps_per_graph`` consecutive steps.  Every
+    step reads its position and token column from device counters, so a graph
+    replays unchanged at any position; the longer graph pays the start and end of
+    a graph launch once per ``steps_per_graph`` steps instead of once per step."""
 
     def __init__(self, model: ParallelTransformer, cache: KVCache, tokens: torch.Tensor, use_graph: bool = True,
-                 fused_trunk: bool = True):
+                 fused_trunk: bool = True, steps_per_graph: int = 8):
         self.model = model
         self.cache = cache
         self.tokens = tokens
@@ -90,30 +94,45 @@ class DecodeGraph:
         if fused_trunk:
             self.bufs.plan = maybe_plan(model, cache, self.bufs.ids, self.bufs.h)
         self.use_graph = use_graph
-        self.graph = None
-        self.logits = None
+        self.steps_per_graph = max(1, int(steps_per_graph))
+        self.graph = None           # (graph, logits of its step)
+        self.graph_n = None         # (graph, logits of its last step)
+        self.logits = None          # logits of the most recent step
 
     def _step(self):
         self.logits = self.model.decode_step(self.bufs, self.cache, self.tokens)
 
     def run(self, n: int):
         """Advance ``n`` tokens (the first call runs one step eagerly, then captures)."""
-        for _ in range(n):
+        S = self.steps_per_graph
+        while n > 0:
+            if self.graph is not None and S > 1 and n >= S:
+                self.cache.check_room(S)
+                if self.graph_n is None:
+                    self.graph_n = self._capture(S)
+                g, self.logits = self.graph_n
+                g.replay()
+                self.cache.length += S
+                n -= S
+                continue
             self.cache.check_room(1)
             if self.graph is not None:
-                self.graph.replay()
+                g, self.logits = self.graph
+                g.replay()
             else:
                 self._step()
                 if self.use_graph:
-                    self._capture()
+                    self.graph = self._capture(1)
             self.cache.length += 1
+            n -= 1
 
-    def _capture(self):
+    def _capture(self, steps: int):
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._step()
-        self.graph = g
+            for _ in range(steps):
+                self._step()
+        return g, self.logits
 
 
 class ParallelExecutor:

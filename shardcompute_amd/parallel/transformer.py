@@ -165,6 +165,8 @@ class StepBuffers:
         if S == 1:
             ws = max(ws, _lib.attention_decode_workspace_bytes(B, H, Hk, D, T_cap))
         self.workspace = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        # greedy-head workspace: zero, and every decode_head call leaves it zero
+        self.head_ws = torch.zeros(_lib.DECODE_HEAD_WORKSPACE_BYTES // 4, dtype=torch.int32, device=dev)
         self.plan = None          # a TrunkPlan when the whole trunk runs as one launch
 
 
@@ -386,6 +388,19 @@ class ParallelTransformer:
         else:
             h = self._embed_sync(bufs.ids, out=bufs.h.view(B, 1, self.hidden_size)).view(B, self.hidden_size)
             h, pending = run_sync(self._trunk(h, cache, B, 1, bufs))
+        lm = self.lm_head
+        if isinstance(lm, QuantizedColumnParallelLinear) and (not lm.gather_output or self.world_size == 1):
+            # final norm, lm_head, greedy selection and counter advance in one call
+            # (at batch 1 the lm_head GEMV selects the token while writing the logits)
+            if lm.quantized_weight is None:
+                raise RuntimeError("Weight not loaded")
+            self.norm._check()
+            logits, _ = _lib.decode_head(h, self.norm.weight, self.norm.eps, lm.quantized_weight, lm.scales,
+                                         lm.biases_quant, bufs.ids.view(-1), bufs.head_ws, residual=pending,
+                                         xn_out=bufs.hn, bias=lm.bias if lm.has_bias else None, bits=lm.bits,
+                                         group_size=lm.group_size, tokens=tokens, step=cache.counters[1:],
+                                         counters=cache.counters, n_counters=2)
+            return logits
         logits = run_sync(self._head(h, pending, B, 1, True, hn_out=bufs.hn))
         _lib.argmax(logits.reshape(B, -1), ids=bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
         _lib.add_i32(cache.counters, 1, n=2)

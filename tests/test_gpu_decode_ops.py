@@ -316,6 +316,7 @@ def test_argmax(device):
     logits[3, 12] = 0x0000                          # ... and one +0.0: equal, index 0 wins
     logits[4] = 0xFF80                              # -inf everywhere but one -1e30
     logits[4, 77777] = 0xF149
+    logits[5, [45, 41 + 8 * 1024, 41]] = 0x4300     # ties within one thread's elements
     ids = torch.empty(6, dtype=torch.int32, device="cuda")
     tokens = torch.full((6, 4), -1, dtype=torch.int32, device="cuda")
     step = torch.tensor([2], dtype=torch.int32, device="cuda")
@@ -323,9 +324,17 @@ def test_argmax(device):
     torch.cuda.synchronize()
     ref = np.argmax(bf16_to_f32(logits), axis=-1)
     assert np.array_equal(ids.cpu().numpy(), ref)
-    assert ref[1] == 10 and ref[2] == 7 and ref[3] == 0 and ref[4] == 77777
+    assert ref[1] == 10 and ref[2] == 7 and ref[3] == 0 and ref[4] == 77777 and ref[5] == 41
     t = tokens.cpu().numpy()
     assert np.array_equal(t[:, 2], ref) and (t[:, [0, 1, 3]] == -1).all()
+    # longer rows: a thread's elements span several load batches; a tie between two
+    # batches of the same thread, and a lone maximum in the last batch
+    big = _bf(rng, (3, 300000))
+    big[1, [8 * (3 + 1024 * 33) + 1, 8 * (3 + 1024 * 20) + 5]] = 0x4300
+    big[2, 299999] = 0x4300
+    got = _lib.argmax(dev_bf16(big)).cpu().numpy()
+    ref = np.argmax(bf16_to_f32(big), axis=-1)
+    assert np.array_equal(got, ref) and ref[1] == 8 * (3 + 1024 * 20) + 5 and ref[2] == 299999
     # odd vocabulary (scalar path)
     small = _bf(rng, (3, 1001))
     got = _lib.argmax(dev_bf16(small)).cpu().numpy()

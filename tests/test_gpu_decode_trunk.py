@@ -170,6 +170,35 @@ def test_trunk_graph_replay_equals_eager(small_w4):
     assert torch.equal(outs[0][2], outs[1][2])
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_multi_step_graph_equals_eager(small_w4, fused):
+    # 13 steps: one eager step, then replays of a 4-step graph (run(4), run(8)) mixed
+    # with single-step replays (run(3), the tail), with eager work in between
+    m = small_w4
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    ids = torch.randint(0, m.vocab_size, (1, 30), generator=gen, device="cuda")
+    ca = m.new_cache(1, 128)
+    logits, _ = asyncio.run(m.forward(ids, past_key_values=ca, use_cache=True, last_only=True))
+    cb = clone_cache(m, ca)
+    outs = []
+    for c, use_graph in ((ca, False), (cb, True)):
+        print(f"multi-step graph: fused trunk {fused}, graphs {use_graph}", flush=True)
+        t = torch.zeros((1, 16), dtype=torch.int32, device="cuda")
+        d = DecodeGraph(m, c, t, use_graph=use_graph, fused_trunk=fused, steps_per_graph=4)
+        _lib.argmax(logits.reshape(1, -1), ids=d.bufs.ids.view(-1), tokens=t, step=c.counters[1:])
+        _lib.add_i32(c.counters[1:], 1, n=1)
+        for n in (1, 4, 3, 8, 1):
+            d.run(n)
+            torch.cuda.synchronize()
+        assert c.length == 30 + 17 and c.counters[:2].tolist() == [47, 18]
+        assert d.bufs.plan is None or d.bufs.plan.status() == 0
+        outs.append((t.clone(), c.k.clone(), c.vt.clone(), d.logits.clone()))
+    assert use_graph and cb.length == ca.length
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
+
+
 def test_trunk_matches_per_op_w8():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
