@@ -5,15 +5,16 @@ Workload: random-init Llama-3-8B shape (hidden 4096, intermediate 14336, 32
 layers, 32 q / 8 kv heads of 128, vocab 128256, RoPE theta 500000, RMSNorm eps
 1e-5), every linear N(0, 0.02) quantized to MLX affine 4-bit g64 on the GPU,
 bf16 vocab embedding, W4 lm_head.  A 2048-token uniform-random prompt is
-prefilled (timed separately), then greedy decode runs as one HIP-graph replay
-per token.  A "step" is one decode token for the whole batch.
+prefilled (timed separately), then greedy decode runs as HIP-graph replays of 8
+steps each.  A "step" is one decode token for the whole batch.
 
 Printed (one JSON line on stdout):
 * ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
   bracketed by device synchronisation);
 * ``roofline``: the dominant kernel of a decode step.  At batch 1 that is the
   whole-trunk launch ``decode_step_kernel<4>`` (embedding and every layer in one
-  persistent kernel; the step adds the final RMSNorm + lm_head GEMV and argmax):
+  persistent kernel; the step adds the final RMSNorm + lm_head GEMV, which also
+  selects the greedy token):
   algorithmic bytes per launch (every layer's packed weights + bf16 scales and
   biases, the KV cache read at the step's length, the appended key/value, the
   embedding row and the output row) over the average launch duration: HIP events
@@ -508,13 +509,13 @@ def main():
                                f"prefill", "batch": B, "prefill_tokens": P, "layers": args.layers,
                    "hidden": cfg["hidden"], "intermediate": cfg["inter"], "heads": cfg["heads"],
                    "kv_heads": cfg["kv_heads"], "vocab": cfg["vocab"], "weights": f"W{args.bits} g64, bf16 s/b",
-                   "activations": "bf16, fp32 accumulate", "decode": "HIP graph replay per token"},
+                   "activations": "bf16, fp32 accumulate", "decode": "HIP graph replays of 8 steps"},
         "roofline": roof,
         "qgemv_roofline": qroof,
         "cpu_baseline": cpu,
         "prefill": {"tokens": B * P, "ms": round(prefill_s * 1e3, 2), "tok_s": round(B * P / prefill_s, 1),
                     "qgemm_roofline": gemm},
-        "decode_step": {"path": "whole-trunk launch + lm_head GEMV + argmax" if trunk is not None
+        "decode_step": {"path": "whole-trunk launch + lm_head GEMV with the greedy selection" if trunk is not None
                         else "per-op launches", "gemv_ms": round(step_gemv_ms, 4), "gemv_bytes": int(step_gemv_bytes),
                         "kv_bytes_avg": int(kv_bytes),
                         "step_hbm_frac": round((step_gemv_bytes + kv_bytes) / (ms_step * 1e-3) / 1e9
