@@ -239,25 +239,34 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
         }
     }
 
-    // ---- epilogue: lane (column li, half lh) register r holds row 8 * (r / 4) + 4 * lh + r % 4
+    // ---- epilogue: lane (column li, half lh) register r holds row 8 * (r / 4) + 4 * lh + r % 4;
+    // registers r, r + 1 (rows dm, dm + 1) round to bf16 in one conversion (RNE), and
+    // the bias is added to the rounded value and rounded again.  Rows are checked
+    // against M only in the last m-tile.
+    const int mw = m0 + wm * 128 + 4 * lh;              // row of register 0 of block i = 0
+    auto store_tile = [&](auto checked) {
+        constexpr bool CHK = decltype(checked)::value;
 #pragma unroll
-    for (int j = 0; j < Gm::NJ; ++j) {
-        const int n = n0 + wn * Gm::WN + j * 32 + li;
-        if (n >= N) continue;
-        const float bb = a.bias ? bf2f(a.bias[n]) : 0.f;
+        for (int j = 0; j < Gm::NJ; ++j) {
+            const int n = n0 + wn * Gm::WN + j * 32 + li;
+            if (n >= N) continue;
+            const float bb = a.bias ? bf2f(a.bias[n]) : 0.f;
+            uint16_t *yc = a.y + (size_t)mw * N + n;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < 4; ++i) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (m < M) {
-                    uint32_t o = f2bf(acc[i][j][r]);
-                    if (a.bias) o = f2bf(bf2f(o) + bb);
-                    a.y[(size_t)m * N + n] = (uint16_t)o;
+                for (int r = 0; r < 16; r += 2) {
+                    uint32_t o = cvt_pk_bf16(acc[i][j][r], acc[i][j][r + 1]);
+                    if (a.bias) o = cvt_pk_bf16(bf2f(o & 0xFFFFu) + bb, bf2f(o >> 16) + bb);
+                    const int dm = i * 32 + 8 * (r >> 2) + (r & 3);
+                    if (!CHK || mw + dm < M) yc[(size_t)dm * N] = (uint16_t)o;
+                    if (!CHK || mw + dm + 1 < M) yc[(size_t)(dm + 1) * N] = (uint16_t)(o >> 16);
                 }
             }
         }
-    }
+    };
+    if (m0 + BM <= M) store_tile(std::false_type{});
+    else store_tile(std::true_type{});
 }
 
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
