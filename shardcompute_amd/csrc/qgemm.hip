@@ -139,6 +139,11 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
         r.s = ssrc[g];
         r.b = bsrc[g];
     };
+    // The nibble mask lives in an SGPR the compiler cannot see through: with a literal
+    // it knows the masked bytes' upper halves are zero and converts bytes 1-3 with a
+    // field extract plus a byte-0 conversion, instead of one v_cvt_f32_ubyteN each.
+    uint32_t nib = 0x0F0F0F0Fu;
+    asm volatile("" : "+s"(nib));
     // dequantize quarter qt (CPT / 4 codes) of a thread's codes into weight buffer buf
     auto store_w = [&](const WRegs<BITS, CPT> &r, int buf, int qt) {
         uint8_t *B = smem + buf * Gm::STAGE + XTILE;
@@ -149,14 +154,14 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
 #pragma unroll
             for (int h = 0; h < QC / 8; ++h) {
                 const uint32_t w = r.w[qt * (QC / 8) + h];
-                const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;   // codes 0,2,4,6 / 1,3,5,7
+                const uint32_t lo = w & nib, hi = (w >> 4) & nib;                   // codes 0,2,4,6 / 1,3,5,7
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     out[h * 4 + j] = cvt_pk_bf16(fmaf(sf, ubyte_f32(lo, j), bf), fmaf(sf, ubyte_f32(hi, j), bf));
             }
             if (QC == 4) {   // half a word per quarter
                 const uint32_t w = r.w[qt >> 1] >> (16 * (qt & 1));
-                const uint32_t lo = w & 0x0F0Fu, hi = (w >> 4) & 0x0F0Fu;
+                const uint32_t lo = w & nib & 0xFFFFu, hi = (w >> 4) & nib & 0xFFFFu;
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     out[j] = cvt_pk_bf16(fmaf(sf, ubyte_f32(lo, j), bf), fmaf(sf, ubyte_f32(hi, j), bf));
