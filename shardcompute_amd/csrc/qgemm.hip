@@ -281,10 +281,15 @@ int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
     if (K % BK) return set_error(SC_EINVAL, "qgemm: K=%d not a multiple of %d", K, BK);
     if (((uintptr_t)x % 16) || ((uintptr_t)wq % 16))
         return set_error(SC_EINVAL, "qgemm: x and wq must be 16-byte aligned");
-    // 256-wide tiles when they already give every CU work, else 128-wide
+    // The tile width with the shorter estimated time: waves of tiles over the CUs times
+    // the cost of one tile, a 128-wide tile costing 0.64 of a 256-wide one (measured
+    // on the Llama-3-8B shapes at M = 2048: it reads more LDS per MFMA).  One partial
+    // wave of wide tiles beats two waves of narrow ones.
     const int cus = device_info().num_cus;
     const int mt = (M + BM - 1) / BM;
-    const bool wide = (long)mt * ((N + 255) / 256) >= cus;
+    const long waves256 = ((long)mt * ((N + 255) / 256) + cus - 1) / cus;
+    const long waves128 = ((long)mt * ((N + 127) / 128) + cus - 1) / cus;
+    const bool wide = 100 * waves256 <= 64 * waves128;
     const int BNv = wide ? 256 : 128;
     const int lds = wide ? Geo<256>::LDS : Geo<128>::LDS;
     if (device_info().max_lds_per_block < lds) return set_error(SC_EUNSUPPORTED, "qgemm: LDS too small");
