@@ -192,23 +192,35 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
     const int li = lane & 31, lh = lane >> 5;
     // one stage: MFMAs of stage g (buffer buf) with the dequant of the next stage's
     // weights (wnext, into buf ^ 1) interleaved a quarter per 16-k step
+    // The operand reads of step ks + 1 are issued before step ks's MFMAs and weight
+    // stores (the compiler cannot move LDS reads above LDS stores it cannot prove
+    // disjoint), so their latency hides behind the MFMAs.  This takes a second set of
+    // operand registers, which W8 with 256-wide tiles does not have to spare; measured
+    // on W4 at M = 2048, 256-wide tiles gain 1-5 % and 128-wide ones lose 1-2 %.
+    constexpr bool AHEAD = BITS == 4 && BN == 256;
     auto stage = [&](int buf, const WRegs<BITS, CPT> &wnext) {
         const uint8_t *A = smem + buf * Gm::STAGE;
         const uint8_t *Bt = A + XTILE;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+        bf16x8_t af[2][4], bfr[2][Gm::NJ];
+        auto frag = [&](int ks, int p) {
             const int chunk = ks * 2 + lh;
-            bf16x8_t af[4], bfr[Gm::NJ];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                af[i] = as_bf16x8(*reinterpret_cast<const uint4 *>(A + swz(wm * 128 + i * 32 + li, chunk)));
+                af[p][i] = as_bf16x8(*reinterpret_cast<const uint4 *>(A + swz(wm * 128 + i * 32 + li, chunk)));
 #pragma unroll
             for (int j = 0; j < Gm::NJ; ++j)
-                bfr[j] = as_bf16x8(*reinterpret_cast<const uint4 *>(Bt + swz(wn * Gm::WN + j * 32 + li, chunk)));
+                bfr[p][j] = as_bf16x8(*reinterpret_cast<const uint4 *>(Bt + swz(wn * Gm::WN + j * 32 + li, chunk)));
+        };
+        if (AHEAD) frag(0, 0);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int p = AHEAD ? (ks & 1) : 0;
+            if (!AHEAD) frag(ks, 0);
+            else if (ks + 1 < 4) frag(ks + 1, p ^ 1);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < Gm::NJ; ++j) acc[i][j] = mfma32x32x16(af[i], bfr[j], acc[i][j]);
+                for (int j = 0; j < Gm::NJ; ++j) acc[i][j] = mfma32x32x16(af[p][i], bfr[p][j], acc[i][j]);
             store_w(wnext, buf ^ 1, ks);
         }
     };
