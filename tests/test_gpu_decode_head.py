@@ -27,15 +27,23 @@ def _bf(rng, shape, scale=1.0):
     return f32_to_bf16((rng.standard_normal(shape) * scale).astype(np.float32))
 
 
-@pytest.mark.parametrize("M,N,K,bits", [(1, 128256, 4096, 4), (1, 32000, 2048, 4), (1, 1000, 512, 8),
-                                        (1, 520, 576, 4), (3, 5000, 1024, 4)])
-def test_decode_head_matches_separate_calls(device, M, N, K, bits):
+@pytest.mark.parametrize("M,N,K,bits,with_bias", [(1, 128256, 4096, 4, False), (1, 32000, 2048, 4, False),
+                                                  (1, 1000, 512, 8, False), (1, 520, 576, 4, False),
+                                                  (3, 5000, 1024, 4, False), (1, 4000, 1024, 4, True),
+                                                  (2, 4000, 1024, 4, True)])
+def test_decode_head_matches_separate_calls(device, M, N, K, bits, with_bias):
     rng = np.random.default_rng(N + K + M)
     w = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     tied = [N // 2 + 1, 5, N - 3]                      # equal rows, far apart: index 5 must win
     w[tied] = 0.05
     wq, s, b = quantize_bf16(w, 64, bits)
     W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    # a linear bias is added to the rounded product; equal on the tied rows
+    bias = None
+    if with_bias:
+        bh = _bf(rng, (N,), 0.5)
+        bh[tied] = bh[5]
+        bias = dev_bf16(bh)
     nw = dev_bf16(f32_to_bf16((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)))
     eps = 1e-5
     ws = torch.zeros(_lib.DECODE_HEAD_WORKSPACE_BYTES // 4, dtype=torch.int32, device="cuda")
@@ -56,9 +64,9 @@ def test_decode_head_matches_separate_calls(device, M, N, K, bits):
         else:
             x, r, nw_c = _bf(rng, (M, K)), dev_bf16(_bf(rng, (M, K))), nw
         xd = dev_bf16(x)
-        logits, xn = _lib.decode_head(xd, nw_c, eps, *W, ids, ws, residual=r, bits=bits, tokens=tokens,
-                                      step=counters[1:], counters=counters, n_counters=2)
-        y_ref, xn_ref = _lib.qmm_rmsnorm(xd, nw_c, eps, *W, residual=r, bits=bits)
+        logits, xn = _lib.decode_head(xd, nw_c, eps, *W, ids, ws, residual=r, bias=bias, bits=bits,
+                                      tokens=tokens, step=counters[1:], counters=counters, n_counters=2)
+        y_ref, xn_ref = _lib.qmm_rmsnorm(xd, nw_c, eps, *W, residual=r, bias=bias, bits=bits)
         _lib.argmax(y_ref, ids=ids_ref, tokens=tokens_ref, step=counters_ref[1:])
         _lib.add_i32(counters_ref, 1, n=2)
         torch.cuda.synchronize()
