@@ -18,7 +18,8 @@ HIP library replaces:
   implementation and as the timed CPU baseline.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
-leg may import anything from here, and only as the checker.  The product path
+leg may import anything from here, and only to check results against (or, for
+the baseline, to time the CPU), never as the thing measured.  The product path
 (``shardcompute_amd``) never imports it: it fails loudly when the HIP library
 is missing instead of falling back to the CPU.
 
