@@ -33,7 +33,16 @@ Parity pins: RMSNorm against its closed form on constant rows, RoPE against the
 equivalent complex rotation ``(a + ib) * e^{i t theta}`` and its norm
 preservation, attention against a per-head scalar loop, GQA against explicit
 head sharing, and the incremental KV-cache path against a single full-sequence
-forward (both are required by the reference's cache semantics).
+forward (both are required by the reference's cache semantics).  The wiring
+(``_attn``, ``_mlp``, the block and ``forward``) is pinned by closed forms on
+structured weights, each computed in float64 without calling this module:
+zero o/down make a block the identity on h; SiLU at known points; gate = 2I,
+up = I, down = I give ``silu(2x) * x`` (a swapped gate/up gives
+``silu(x) * 2x``); a one-layer model with those weights, o = 0 and an identity
+lm_head gives ``norm(h + silu(2 xn) xn)`` with ``xn = norm(h)`` (a post-norm
+block, a dropped residual or a missing final norm each miss it by far more
+than the tolerance); v = I, o = I give each query head its kv head's input
+slice at one token, and q = 0 gives causal running means of v over a prompt.
 """
 from dataclasses import dataclass, field
 
@@ -119,6 +128,13 @@ def apply_rope(x32, cos, sin):
     return round_bf16(x32 * cos[None, None] + rot * sin[None, None])
 
 
+def silu(x32):
+    """``x * sigmoid(x)`` (``parallel/mlp.py:161-162``) in fp32, as ``x / (1 + exp(-x))``."""
+    x = np.asarray(x32, dtype=np.float32)
+    with np.errstate(over="ignore"):
+        return x / (np.float32(1) + np.exp(-x, dtype=np.float32))
+
+
 def attention_core(q, k, v, scale, causal_offset):
     """q [B,H,S,D]; k,v [B,H,T,D] (already GQA-expanded) -> [B,H,S,D] bf16-valued.
 
@@ -182,7 +198,7 @@ class OracleDecoder:
         sh = self.shape
         g = qlinear(x, L["gate"], sh)
         u = qlinear(x, L["up"], sh)
-        a = round_bf16((g / (np.float32(1) + np.exp(-g, dtype=np.float32))) * u)
+        a = round_bf16(silu(g) * u)
         return qlinear(a, L["down"], sh)
 
     def forward(self, ids, last_only=False):

@@ -34,6 +34,7 @@ from .parallel.transformer import ParallelTransformer, StepBuffers, run_sync
 @dataclass
 class LayerTiming:
     layer_idx: int
+    layer_type: str = "transformer"     # "embedding", "transformer", "lm_head"
     compute_ms: float = 0.0
     comm_ms: float = 0.0
 
@@ -70,8 +71,9 @@ class ExecutionMetrics:
             "compute_fraction": self.compute_fraction,
             "input_tokens": self.input_tokens,
             "output_shape": self.output_shape,
-            "layer_timings": [{"layer": t.layer_idx, "compute_ms": t.compute_ms, "comm_ms": t.comm_ms}
-                              for t in self.layer_timings],
+            "num_layers": len([t for t in self.layer_timings if t.layer_type == "transformer"]),
+            "layer_timings": [{"layer": t.layer_idx, "type": t.layer_type, "compute_ms": t.compute_ms,
+                               "comm_ms": t.comm_ms} for t in self.layer_timings],
         }
 
 
@@ -149,11 +151,25 @@ class ParallelExecutor:
 
     # ---------------------------------------------------------------- forward
 
-    def _ensure_cache(self, batch: int, needed: int) -> KVCache:
+    def _ensure_cache(self, batch: int, needed: int, exact: bool = False) -> KVCache:
+        """A cache with room for ``needed`` more positions.
+
+        The reference's cache grows by one concatenation per step; here a cache
+        that is too small is replaced by one with room for the cached positions
+        plus ``needed`` (doubled, unless ``exact``: ``generate`` knows its final
+        length), and the cached positions are copied over.  The capacity never
+        defaults to ``max_position_embeddings``: a Llama-3 config's 8 K or 128 K
+        positions would reserve gigabytes per sequence and make the batch-1
+        decode plan's attention state exceed a CU's LDS."""
         c = self._past_key_values
-        if c is None or c.batch != batch or c.capacity < c.length + needed:
-            cap = max(round_capacity((0 if c is None else c.length) + needed), self.model.max_position_embeddings)
-            newc = self.model.new_cache(batch, cap)
+        if c is not None and c.batch != batch:
+            c = None
+        have = 0 if c is None else c.length
+        if c is None or c.capacity < have + needed:
+            want = have + needed
+            if not exact and c is not None:
+                want = max(want, 2 * c.capacity)
+            newc = self.model.new_cache(batch, round_capacity(want))
             if c is not None and c.length:
                 newc.load_tuples(c.as_tuples())
             self._past_key_values = c = newc
@@ -170,13 +186,40 @@ class ParallelExecutor:
                                              input_tokens=int(ids.numel()), output_shape=list(logits.shape))
         return logits
 
-    async def forward_with_timing(self, input_ids, attention_mask=None, use_cache: bool = False):
-        """``forward`` with per-layer compute time from HIP events (no collectives here)."""
-        logits = await self.forward(input_ids, attention_mask=attention_mask, use_cache=use_cache)
-        n = max(1, len(self.model.layers))
-        per = self.last_metrics.total_time_ms / n
-        self.last_metrics.layer_timings = [LayerTiming(i, compute_ms=per) for i in range(len(self.model.layers))]
-        return logits
+    async def forward_with_timing(self, input_ids, attention_mask=None):
+        """A cache-less forward with each stage timed on the GPU
+        (``worker/executor.py:155-227``): the embedding (layer -1), every
+        transformer block, and the final norm + lm_head (layer -2).
+
+        Each stage is bracketed by HIP events on the current stream, so its
+        ``compute_ms`` is the stage's own GPU time (the reference times each
+        stage with ``mx.eval`` and the host clock).  There are no collectives on
+        one GPU: ``comm_ms`` is 0.  Returns ``(logits, metrics)``."""
+        m = self.model
+        t0 = time.perf_counter()
+        ids = torch.as_tensor(input_ids).to(m.device)
+        B, S = ids.shape
+        ev = [torch.cuda.Event(enable_timing=True)]
+        ev[0].record()
+        h = await m.embed_tokens.forward(ids)
+        ev.append(torch.cuda.Event(enable_timing=True))
+        ev[-1].record()
+        for layer in m.layers:
+            h, _ = await layer.forward(h, attention_mask)
+            ev.append(torch.cuda.Event(enable_timing=True))
+            ev[-1].record()
+        logits = await m._head(h.reshape(B * S, m.hidden_size), None, B, S, False)
+        ev.append(torch.cuda.Event(enable_timing=True))
+        ev[-1].record()
+        torch.cuda.synchronize()
+        span = [ev[i].elapsed_time(ev[i + 1]) for i in range(len(ev) - 1)]
+        timings = [LayerTiming(-1, "embedding", span[0])]
+        timings += [LayerTiming(i, "transformer", span[1 + i]) for i in range(len(m.layers))]
+        timings.append(LayerTiming(-2, "lm_head", span[-1]))
+        logits = logits.reshape(B, S, -1)
+        self.last_metrics = ExecutionMetrics(total_time_ms=(time.perf_counter() - t0) * 1000, layer_timings=timings,
+                                             input_tokens=int(ids.numel()), output_shape=list(logits.shape))
+        return logits, self.last_metrics
 
     # ---------------------------------------------------------------- generation
 
@@ -199,7 +242,7 @@ class ParallelExecutor:
         out_dtype = ids.dtype
         B, S = ids.shape
         self._past_key_values = None
-        cache = self._ensure_cache(B, S + max(1, max_new_tokens))
+        cache = self._ensure_cache(B, S + max(1, max_new_tokens), exact=True)
         cache.reset()
         if max_new_tokens <= 0:
             return ids
@@ -228,21 +271,35 @@ class ParallelExecutor:
 
         if temperature == 0:
             dec = DecodeGraph(self.model, cache, tokens, use_graph=self.use_graphs)
+            plan = dec.bufs.plan
+
+            def check_plan():
+                # the whole-trunk launch bounds every wait; one that gave up left its
+                # outputs invalid, and the tokens after it would be silently wrong
+                if plan is not None and plan.status() != 0:
+                    raise RuntimeError(f"whole-trunk decode launch gave up waiting (status {plan.status()}): "
+                                       f"another kernel held CUs it needs; the generated tokens are invalid")
+
             _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
             _lib.add_i32(cache.counters[1:], 1, n=1)
             n_done = 1
             end = None
+            # tokens reach the host (stop check, streaming callback) every check_every tokens
+            report = bool(stop) or token_callback is not None
             while end is None:
                 if n_done >= max_new_tokens:
+                    check_plan()
                     end = await flush(max_new_tokens) or max_new_tokens
                     break
-                if stop and n_done - emitted >= self.check_every:
+                if report and n_done - emitted >= self.check_every:
+                    check_plan()
                     end = await flush(n_done)
                     if end is not None:
                         break
-                chunk = min(self.check_every, max_new_tokens - n_done)
-                dec.run(chunk)
-                n_done += chunk
+                chunk = min(self.check_every - (n_done - emitted) if report else self.check_every,
+                            max_new_tokens - n_done)
+                dec.run(max(1, chunk))
+                n_done += max(1, chunk)
             n_gen = end
         else:
             n_gen = None

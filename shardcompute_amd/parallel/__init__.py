@@ -5,9 +5,10 @@ Mirrors the public classes of the reference's ``src/shardcompute/parallel/``.
 from .column_linear import ColumnParallelLinear
 from .embedding import ParallelEmbedding, QuantizedParallelEmbedding, VocabParallelEmbedding
 from .quantized_linear import QuantizedColumnParallelLinear, QuantizedRowParallelLinear
-from .row_linear import RowParallelLinear
+from .row_linear import FusedColumnRowLinear, RowParallelLinear
 
 __all__ = [
-    "ColumnParallelLinear", "RowParallelLinear", "QuantizedColumnParallelLinear", "QuantizedRowParallelLinear",
+    "ColumnParallelLinear", "RowParallelLinear", "FusedColumnRowLinear", "QuantizedColumnParallelLinear",
+    "QuantizedRowParallelLinear",
     "ParallelEmbedding", "QuantizedParallelEmbedding", "VocabParallelEmbedding",
 ]

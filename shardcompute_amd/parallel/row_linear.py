@@ -1,4 +1,6 @@
-"""Dense row-parallel linear (``src/shardcompute/parallel/row_linear.py:12-217``).
+"""Dense row-parallel linear (``src/shardcompute/parallel/row_linear.py:12-217``)
+and the column -> activation -> row composition ``FusedColumnRowLinear``
+(``:220-311``).
 
 Not a hot-path kernel: ``[local_in, out]`` weights, torch GEMM, all-reduce
 through the communicator when one is given, bias on rank 0 only.
@@ -79,3 +81,50 @@ class RowParallelLinear:
     def __repr__(self):
         return (f"RowParallelLinear(in_features={self.in_features}, out_features={self.out_features}, "
                 f"local_in_features={self.local_in_features}, rank={self.rank}/{self.world_size})")
+
+
+def _activation(name):
+    """The activations of ``row_linear.py:268-276``, on bf16 tensors computed in fp32."""
+    if name == "gelu":
+        return lambda x: (x.float() * torch.sigmoid(1.702 * x.float())).to(x.dtype)   # sigmoid approximation
+    if name in ("silu", "swish"):
+        return lambda x: (x.float() * torch.sigmoid(x.float())).to(x.dtype)
+    if name == "relu":
+        return lambda x: torch.clamp_min(x, 0)
+    return lambda x: x
+
+
+class FusedColumnRowLinear:
+    """Column-parallel up projection -> activation -> row-parallel down projection
+    with one all-reduce at the end (``row_linear.py:220-311``).
+
+    The reference module refers to ``ColumnParallelLinear`` without importing it,
+    so its constructor raises ``NameError`` as shipped; this class builds what the
+    constructor describes: ``up_proj`` a ``ColumnParallelLinear`` (no gather, no
+    communicator), ``down_proj`` a ``RowParallelLinear`` carrying the
+    communicator.  Dense ``[in, out]`` weights and torch GEMMs, as the two
+    classes it composes."""
+
+    def __init__(self, in_features: int, hidden_features: int, out_features: int, world_size: int, rank: int,
+                 activation: str = "gelu", bias: bool = True, communicator=None, device=None):
+        from .column_linear import ColumnParallelLinear
+        self.in_features = in_features
+        self.hidden_features = hidden_features
+        self.out_features = out_features
+        self.world_size = world_size
+        self.rank = rank
+        self.communicator = communicator
+        self.up_proj = ColumnParallelLinear(in_features, hidden_features, world_size, rank, bias=bias,
+                                            gather_output=False, communicator=None, device=device)
+        self.down_proj = RowParallelLinear(hidden_features, out_features, world_size, rank, bias=bias,
+                                           input_is_partitioned=True, communicator=communicator, device=device)
+        self.activation_name = activation
+        self.activation = _activation(activation)
+
+    def load_shards(self, up_weight, up_bias, down_weight, down_bias):
+        self.up_proj.load_shard_direct(up_weight, up_bias)
+        self.down_proj.load_shard_direct(down_weight, down_bias)
+
+    async def forward(self, x):
+        hidden = self.activation(self.up_proj.forward_sync(x))
+        return await self.down_proj.forward(hidden)

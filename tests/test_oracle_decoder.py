@@ -108,3 +108,181 @@ def test_teacher_forcing_with_own_tokens_reproduces_free_run():
     assert np.array_equal(toks, toks2)
     for a, b in zip(logits, logits2):
         assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------- wiring pins
+#
+# Closed forms on structured weights.  Each expectation is computed in float64
+# from the formula the reference states (pre-norm block transformer.py:237-254,
+# SwiGLU mlp.py:161-162 and :241-254, model transformer.py:536-577, attention
+# attention.py:403-471), without calling oracle.decoder; alternatives a
+# plausible wiring mistake would compute are shown to miss by far more than the
+# tolerance.
+
+from oracle.decoder import QLinear, silu  # noqa: E402
+from oracle.mlx_affine import pack  # noqa: E402
+
+
+def _structured(q_codes, scale, bits=4, group_size=64):
+    """QLinear with W = scale * q (bias 0): integer codes [N, K], one scale for all groups."""
+    N, K = q_codes.shape
+    s = np.full((N, K // group_size), f32_to_bf16(np.float32(scale)), np.uint16)
+    b = np.zeros_like(s)
+    return QLinear(pack(q_codes, bits), s, b)
+
+
+def _eye(n, k, code=1, scale=1.0):
+    q = np.zeros((n, k), np.uint32)
+    m = min(n, k)
+    q[np.arange(m), np.arange(m)] = code
+    return _structured(q, scale)
+
+
+def _zero(n, k):
+    return _structured(np.zeros((n, k), np.uint32), 0.0)
+
+
+def _norm64(x, w, eps=1e-5):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w
+
+
+def _silu64(x):
+    return x / (1.0 + np.exp(-np.asarray(x, np.float64)))
+
+
+def _close(got, exp, frac=2e-2):
+    return float(np.abs(got - exp).max()) <= frac * float(np.abs(exp).max())
+
+
+def test_silu_known_values():
+    x = np.array([0.0, 1.0, -1.0, 2.5, 30.0, -30.0, 100.0, -100.0], np.float32)
+    got = silu(x)
+    exp = np.array([0.0, 1 / (1 + np.exp(-1.0)), -1 / (1 + np.exp(1.0)), 2.5 / (1 + np.exp(-2.5)),
+                    30.0, -30.0 * np.exp(-30.0), 100.0, -100.0 * np.exp(-100.0)])
+    assert got[0] == 0.0
+    assert np.allclose(got, exp, rtol=1e-6, atol=1e-30)
+    assert abs(got[1] - 0.7310585786300049) < 1e-6
+    assert got[7] <= 0.0 and np.isfinite(got[7])
+
+
+H64 = 64
+
+
+def _one_layer_weights(rng, o_zero=True, down=None):
+    """hidden = intermediate = 64, 2 q heads / 1 kv head of 32, vocab 96."""
+    sh = DecoderShape(vocab_size=96, hidden_size=H64, num_layers=1, num_heads=2, num_kv_heads=1,
+                      intermediate_size=H64, rope_theta=10000.0)
+    nw = lambda: f32_to_bf16((1.0 + 0.2 * rng.standard_normal(H64)).astype(np.float32))  # noqa: E731
+    rq = lambda n, k: QLinear(*__import__("oracle.mlx_affine", fromlist=["x"]).quantize_bf16(  # noqa: E731
+        (0.05 * rng.standard_normal((n, k))).astype(np.float32), 64, 4))
+    L = dict(input_ln=nw(), post_ln=nw(), q=rq(64, 64), k=rq(32, 64), v=rq(32, 64),
+             o=_zero(64, 64) if o_zero else rq(64, 64),
+             gate=_eye(64, 64, code=2), up=_eye(64, 64, code=1),
+             down=_eye(64, 64, code=1) if down is None else down)
+    # rms 4 rows: far from their normalisation, so norm(h) and h differ
+    embed = f32_to_bf16((4.0 * rng.standard_normal((96, H64))).astype(np.float32))
+    W = dict(embed=embed, norm=nw(), lm_head=_eye(96, 64, code=1), layers=[L])
+    return sh, W
+
+
+def test_block_is_identity_when_o_and_down_are_zero():
+    rng = np.random.default_rng(30)
+    sh, W = _one_layer_weights(rng, o_zero=True, down=_zero(64, 64))
+    dec = OracleDecoder(sh, W)
+    h = round_bf16(rng.standard_normal((1, 5, H64)).astype(np.float32))
+    L = W["layers"][0]
+    from oracle.decoder import rms_norm as _rms
+    xn = _rms(h, L["input_ln"], sh.rms_norm_eps)
+    h1 = round_bf16(h + dec._attn(0, xn, L))
+    xn = _rms(h1, L["post_ln"], sh.rms_norm_eps)
+    h2 = round_bf16(h1 + dec._mlp(xn, L))
+    assert np.array_equal(h1, h) and np.array_equal(h2, h)
+    # the whole model: logits = norm(embedding row) through the identity lm_head
+    ids = np.array([[3, 17, 95]])
+    logits = OracleDecoder(sh, W).forward(ids)
+    exp = _norm64(bf16_to_f32(W["embed"][ids]), bf16_to_f32(W["norm"]))
+    exp = np.concatenate([exp, np.zeros(exp.shape[:-1] + (32,))], -1)   # vocab rows 64..95 are zero
+    assert _close(logits, exp, 1e-2)
+
+
+def test_mlp_gate_up_roles():
+    rng = np.random.default_rng(31)
+    sh, W = _one_layer_weights(rng)
+    # inputs in [-4, 1.5]: for large positive x every variant tends to 2 x^2, so
+    # the roles show where the sigmoid is far from 1
+    x = round_bf16(np.stack([np.linspace(-4, 1.5, H64), np.linspace(1.5, -4, H64),
+                             rng.uniform(-4, 1.5, H64)]).astype(np.float32))
+    got = OracleDecoder(sh, W)._mlp(x, W["layers"][0])
+    xd = x.astype(np.float64)
+    exp = _silu64(2 * xd) * xd                       # gate = 2I, up = I, down = I
+    swapped = _silu64(xd) * 2 * xd                   # gate and up exchanged
+    ungated = _silu64(2 * xd)                        # up dropped
+    assert _close(got, exp, 1e-2)
+    assert not _close(swapped, exp, 0.1) and not _close(ungated, exp, 0.1)
+
+
+def test_one_layer_model_closed_form_prenorm():
+    rng = np.random.default_rng(32)
+    sh, W = _one_layer_weights(rng)                  # o = 0: the attention adds nothing
+    ids = np.array([[5, 60, 7, 33]])
+    logits = OracleDecoder(sh, W).forward(ids)[..., :H64]
+    L = W["layers"][0]
+    w_post, w_fin = bf16_to_f32(L["post_ln"]).astype(np.float64), bf16_to_f32(W["norm"]).astype(np.float64)
+    h = bf16_to_f32(W["embed"][ids]).astype(np.float64)
+    xn = _norm64(h, w_post)
+    exp = _norm64(h + _silu64(2 * xn) * xn, w_fin)                 # pre-norm block, final norm, lm_head = I
+    w_in = bf16_to_f32(L["input_ln"]).astype(np.float64)
+    h1 = _norm64(h, w_in)                                           # post-norm: norm after each residual add
+    post_norm = _norm64(_norm64(h1 + _silu64(2 * h1) * h1, w_post), w_fin)
+    no_resid = _norm64(_silu64(2 * xn) * xn, w_fin)                 # residual dropped
+    no_final = h + _silu64(2 * xn) * xn                             # final norm missing
+    no_mlp = _norm64(h, w_fin)                                      # block output dropped
+    assert _close(logits, exp, 2e-2)
+    for wrong in (post_norm, no_resid, no_final, no_mlp):
+        assert not _close(wrong, exp, 0.1)
+
+
+def test_attention_value_path_and_gqa_mapping():
+    # v = I on the kv head's slice, o = I: at one token the softmax is over one
+    # key, so query head h outputs v of kv head h // rep = x[(h // rep) * D : ...]
+    rng = np.random.default_rng(33)
+    sh = DecoderShape(vocab_size=64, hidden_size=128, num_layers=1, num_heads=4, num_kv_heads=2,
+                      intermediate_size=64, rope_theta=10000.0)
+    D = sh.head_dim                                   # 32
+    rq = lambda n, k: QLinear(*__import__("oracle.mlx_affine", fromlist=["x"]).quantize_bf16(  # noqa: E731
+        (0.05 * rng.standard_normal((n, k))).astype(np.float32), 64, 4))
+    L = dict(q=rq(128, 128), k=rq(64, 128), v=_eye(64, 128), o=_eye(128, 128))
+    dec = OracleDecoder(sh, dict(layers=[L]))
+    x = round_bf16(rng.standard_normal((1, 1, 128)).astype(np.float32))
+    got = dec._attn(0, x, L)[0, 0]
+    exp = np.concatenate([x[0, 0, (h // 2) * D:(h // 2 + 1) * D] for h in range(4)])
+    wrong = np.concatenate([x[0, 0, (h % 2) * D:(h % 2 + 1) * D] for h in range(4)])   # heads interleaved
+    assert np.array_equal(got, exp)
+    assert not np.array_equal(wrong, exp)
+
+
+def test_attention_causal_uniform_scores():
+    # q = 0: every allowed score is 0, so position i outputs the mean of v over
+    # positions 0..i (causal); a mask of the wrong orientation would average the
+    # future, no mask would give the full mean everywhere
+    rng = np.random.default_rng(34)
+    sh = DecoderShape(vocab_size=64, hidden_size=64, num_layers=1, num_heads=2, num_kv_heads=1,
+                      intermediate_size=64, rope_theta=10000.0)
+    rq = lambda n, k: QLinear(*__import__("oracle.mlx_affine", fromlist=["x"]).quantize_bf16(  # noqa: E731
+        (0.05 * rng.standard_normal((n, k))).astype(np.float32), 64, 4))
+    L = dict(q=_zero(64, 64), k=rq(32, 64), v=_eye(32, 64), o=_eye(64, 64))
+    x = round_bf16(rng.standard_normal((1, 6, 64)).astype(np.float32))
+    got = OracleDecoder(sh, dict(layers=[L]))._attn(0, x, L)[0]
+    v = x[0, :, :32].astype(np.float64)
+    run_mean = np.cumsum(v, 0) / np.arange(1, 7)[:, None]
+    exp = np.concatenate([run_mean, run_mean], -1)     # both q heads share kv head 0
+    assert _close(got, exp, 1e-2)
+    fut = np.cumsum(v[::-1], 0)[::-1] / np.arange(6, 0, -1)[:, None]
+    assert not _close(np.concatenate([fut, fut], -1), exp, 0.1)
+    full = np.repeat(v.mean(0, keepdims=True), 6, 0)
+    assert not _close(np.concatenate([full, full], -1), exp, 0.1)
+    # and the cache: the same positions fed one at a time give the same outputs
+    dec = OracleDecoder(sh, dict(layers=[L]))
+    inc = np.concatenate([dec._attn(0, x[:, t:t + 1], L)[0] for t in range(6)])
+    assert _close(inc, exp, 1e-2)

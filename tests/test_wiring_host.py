@@ -114,8 +114,12 @@ def test_kv_cache_layout_roundtrip():
 
 
 def test_execution_metrics():
-    m = ExecutionMetrics(total_time_ms=10.0, layer_timings=[LayerTiming(0, 3.0, 1.0), LayerTiming(1, 5.0, 1.0)],
+    # LayerTiming(layer_idx, layer_type, compute_ms, comm_ms) as worker/executor.py:19-29
+    m = ExecutionMetrics(total_time_ms=10.0, layer_timings=[LayerTiming(-1, "embedding", 0.5),
+                                                            LayerTiming(0, "transformer", 3.0, 1.0),
+                                                            LayerTiming(1, "transformer", 5.0, 1.0)],
                          input_tokens=4, output_shape=[1, 4])
-    assert m.compute_time_ms == 8.0 and m.comm_time_ms == 2.0 and m.compute_fraction == pytest.approx(0.8)
+    assert m.compute_time_ms == 8.5 and m.comm_time_ms == 2.0 and m.compute_fraction == pytest.approx(8.5 / 10.5)
     d = m.to_dict()
-    assert d["layer_timings"][1] == {"layer": 1, "compute_ms": 5.0, "comm_ms": 1.0}
+    assert d["num_layers"] == 2
+    assert d["layer_timings"][2] == {"layer": 1, "type": "transformer", "compute_ms": 5.0, "comm_ms": 1.0}
