@@ -255,10 +255,7 @@ __global__ void __launch_bounds__(64 * DMA_MAX_WAVES) qgemv_dma_kernel(DmaArgs a
 #pragma unroll
             for (int i = 0; i < XMAX; ++i) {
                 const int idx = tid + i * (int)blockDim.x;
-                if (idx < M * W) {
-                    const int m = idx / W, w = idx - (idx / W) * W;
-                    v[i] = raw[idx];
-                }
+                if (idx < M * W) v[i] = raw[idx];
             }
             __syncthreads();                                        // raw rows fully read
 #pragma unroll

@@ -124,7 +124,10 @@ class DecodeGraph:
             else:
                 self._step()
                 if self.use_graph:
+                    eager = self.logits
                     self.graph = self._capture(1)
+                    # capture only records: the step's logits are the eager run's
+                    self.logits = eager
             self.cache.length += 1
             n -= 1
 

@@ -1,0 +1,138 @@
+"""The benchmarked batch-1 decode path against the oracle decoder.
+
+The decode step that ``bench.py`` times is the whole-trunk launch
+(``decode_step_kernel``: embedding and every layer in one persistent kernel)
+followed by the greedy head (final RMSNorm + lm_head GEMV that also selects the
+token).  It only takes head_dim 128 with at most 4 query heads per kv head, so
+this test runs that geometry end to end against ``oracle.decoder.OracleDecoder``
+on the same packed weights:
+
+* the model is prefilled, then decodes greedily through ``DecodeGraph`` with the
+  trunk plan (graph replays of one step), recording every step's logits;
+* the oracle is teacher-forced with the GPU's tokens
+  (``OracleDecoder.generate_greedy(forced=...)``) and every step's logits must be
+  within LOGIT_TOL max-abs-rel; every GPU token must be the oracle's argmax up to
+  a 2 % margin of the logit range, and the exact-argmax agreement must be >= 95 %;
+* the plan's status word stays 0.
+
+Shapes: 16 q / 4 kv heads of 128, hidden 2048, W4 and W8; and two layers of
+the Llama-3-8B shape (hidden 4096, 32 q / 8 kv heads, intermediate 14336), W4.
+Weights are drawn and quantized on the GPU (``sc_quantize_affine``, bit-exact
+with the oracle's quantizer) and copied to the host for the oracle.
+"""
+import asyncio
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_to_f32
+from oracle.decoder import DecoderShape, OracleDecoder, QLinear
+from shardcompute_amd import _lib
+from shardcompute_amd.executor import DecodeGraph
+from shardcompute_amd.parallel.transformer import ParallelTransformer
+from tests.gpu_util import host_u16, host_u32
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_TOL = 3e-2
+
+
+def gpu_model_and_oracle(cfg, bits, capacity, seed=0):
+    """A random-init quantized model on the GPU and the same weights in oracle form."""
+    dev = torch.device("cuda", 0)
+    H, I, V = cfg["hidden"], cfg["inter"], cfg["vocab"]
+    D = H // cfg["heads"]
+    nq, nkv = cfg["heads"] * D, cfg["kv_heads"] * D
+    m = ParallelTransformer(vocab_size=V, hidden_size=H, num_layers=cfg["layers"], num_heads=cfg["heads"],
+                            intermediate_size=I, world_size=1, rank=0, num_kv_heads=cfg["kv_heads"],
+                            max_position_embeddings=capacity, rms_norm_eps=1e-5, rope_base=cfg["theta"],
+                            use_quantized=True, quantization_bits=bits, quantization_group_size=64,
+                            embedding="vocab", quantized_lm_head=True, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+
+    def q(n, k):
+        t = _lib.quantize(torch.randn((n, k), generator=g, device=dev).mul_(0.02), bits=bits)
+        return t, QLinear(host_u32(t[0]), host_u16(t[1]), host_u16(t[2]))
+
+    def norm_w():
+        t = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+        return t, host_u16(t)
+
+    layers = []
+    for layer in m.layers:
+        (li, li_h), (lp, lp_h) = norm_w(), norm_w()
+        layer.input_layernorm.load_weights(li)
+        layer.post_attention_layernorm.load_weights(lp)
+        (qt, qo), (kt, ko), (vt, vo), (ot, oo) = q(nq, H), q(nkv, H), q(nkv, H), q(H, nq)
+        layer.attention.load_quantized_shards(*qt, None, *kt, None, *vt, None, *ot, None)
+        (gt, go), (ut, uo), (dt, do) = q(I, H), q(I, H), q(H, I)
+        layer.mlp.load_quantized_shards(*ut, None, *dt, None, *gt, None)
+        layers.append(dict(input_ln=li_h, post_ln=lp_h, q=qo, k=ko, v=vo, o=oo, gate=go, up=uo, down=do))
+    emb = torch.randn((V, H), generator=g, device=dev).mul_(0.02).to(torch.bfloat16)
+    m.load_embedding_weights(emb)
+    nt, nh = norm_w()
+    m.load_norm_weights(nt)
+    lt, lo = q(V, H)
+    m.load_quantized_lm_head_weights(*lt)
+    torch.cuda.synchronize()
+    shape = DecoderShape(vocab_size=V, hidden_size=H, num_layers=cfg["layers"], num_heads=cfg["heads"],
+                         num_kv_heads=cfg["kv_heads"], intermediate_size=I, rms_norm_eps=1e-5,
+                         rope_theta=cfg["theta"], bits=bits)
+    return m, OracleDecoder(shape, dict(embed=host_u16(emb), norm=nh, lm_head=lo, layers=layers))
+
+
+def trunk_greedy(model, prompt, steps):
+    """Prefill, then ``steps`` greedy decode steps through the whole-trunk plan.
+    Returns (tokens [steps + 1], list of steps + 1 last-position logits)."""
+    B, S = prompt.shape
+    cache = model.new_cache(B, S + steps + 32)
+    ids = torch.from_numpy(prompt.astype(np.int64)).cuda()
+    logits, _ = asyncio.run(model.forward(ids, past_key_values=cache, use_cache=True, last_only=True))
+    tokens = torch.zeros((B, steps + 2), dtype=torch.int32, device="cuda")
+    dec = DecodeGraph(model, cache, tokens, use_graph=True, fused_trunk=True)
+    assert dec.bufs.plan is not None, "the whole-trunk plan must apply to this model"
+    _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
+    _lib.add_i32(cache.counters[1:], 1, n=1)
+    out = [bf16_to_f32(host_u16(logits.reshape(B, -1)))]
+    for _ in range(steps):
+        dec.run(1)
+        out.append(bf16_to_f32(host_u16(dec.logits.reshape(B, -1))))
+    torch.cuda.synchronize()
+    assert dec.bufs.plan.status() == 0, "a trunk launch gave up waiting"
+    return tokens[0, :steps + 1].cpu().numpy(), out
+
+
+def compare(model, oracle, prompt_len, steps, seed):
+    V = model.vocab_size
+    prompt = np.random.default_rng(seed).integers(0, V, (1, prompt_len))
+    toks, gl = trunk_greedy(model, prompt, steps)
+    _, ol = oracle.generate_greedy(prompt, steps + 1, forced=toks[None, :])
+    assert len(ol) == len(gl) == steps + 1
+    agree, worst = 0, 0.0
+    for t, (g, o) in enumerate(zip(gl, ol)):
+        o = o[0].astype(np.float64)
+        err = float(np.abs(g[0] - o).max() / np.abs(o).max())
+        worst = max(worst, err)
+        assert err <= LOGIT_TOL, f"step {t}: logits max-abs-rel {err:.3e}"
+        tok = int(toks[t])
+        assert o[tok] >= o.max() - 0.02 * np.abs(o).max(), f"step {t}: token {tok} not near the oracle's argmax"
+        agree += int(tok == int(np.argmax(o)))
+    print(f"trunk vs oracle: worst logits max-abs-rel {worst:.2e}, argmax agreement {agree}/{steps + 1}", flush=True)
+    assert agree >= 0.95 * (steps + 1)
+
+
+SMALL = dict(hidden=2048, inter=2048, heads=16, kv_heads=4, vocab=2048, layers=2, theta=500000.0)
+LLAMA8B_2L = dict(hidden=4096, inter=14336, heads=32, kv_heads=8, vocab=4096, layers=2, theta=500000.0)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_trunk_decode_matches_oracle_small(device, bits):
+    model, oracle = gpu_model_and_oracle(SMALL, bits, 256, seed=bits)
+    compare(model, oracle, prompt_len=37, steps=20, seed=bits)
+
+
+def test_trunk_decode_matches_oracle_llama3_8b_layers(device):
+    model, oracle = gpu_model_and_oracle(LLAMA8B_2L, 4, 256, seed=11)
+    compare(model, oracle, prompt_len=64, steps=12, seed=11)
