@@ -13,11 +13,13 @@
  *  - Return 0 on success, a negative status otherwise (-1 bad argument,
  *    -2 unsupported configuration, -3 HIP runtime error); sc_last_error() then
  *    holds a message (thread-local, valid until the next failing call).
- *  - The kernels allocate nothing per call.  The split-K path of sc_qmm_bf16 uses a
+ *  - The kernels allocate nothing per call.  The split-K path of sc_qmm_bf16 (and of
+ *    the products inside sc_qmm_rmsnorm_bf16 / sc_qmm_swiglu_bf16 at 9-32 rows) uses a
  *    library-owned scratch per device, allocated on first need and grown (with a
  *    device synchronisation) when a larger shape arrives: calls that overlap on one
  *    device (concurrent streams) race on it, and the first call of a new largest
- *    shape must not happen under stream capture.
+ *    shape must not happen under stream capture.  sc_qmm_bf16_noalloc is the
+ *    variant that never allocates.
  */
 #ifndef SHARDCOMPUTE_HIP_H
 #define SHARDCOMPUTE_HIP_H
@@ -28,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 7
+#define SC_ABI_VERSION 8
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -67,6 +69,28 @@ int sc_qmm_bf16(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, c
 int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
                      const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
                      int group_size, int path, void *hip_stream);
+
+/* Size of the device array that sc_qmm_bf16_noalloc's split-K partials live in. */
+#define SC_QMM_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/*
+ * sc_qmm_bf16 that never allocates device memory, for callers that cannot call
+ * hipMalloc: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation.  No counterpart in the reference (mx.quantized_matmul
+ * allocates its output; this entry point allocates nothing at all).  Same
+ * arguments, kernels and results as sc_qmm_bf16, bit for bit.  Where the 9-32-row
+ * GEMV splits K across workgroups, its fp32 partials go to a file-scope device
+ * array of SC_QMM_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process
+ * ends) instead of the library's growable buffer; a shape whose partials
+ * (splits * M * N floats) exceed it returns -1 with a message.  The array's
+ * address is looked up on the first call on each device (no allocation, no
+ * synchronisation).  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (concurrent streams) race.  Each launch writes every
+ * partial it reads, so nothing needs clearing between calls.
+ */
+int sc_qmm_bf16_noalloc(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                        const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                        int group_size, void *hip_stream);
 
 /*
  * Vocab-sharded bf16 row gather: for t < T,

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -23,6 +23,7 @@ EXPORTS = (
     "sc_last_error",
     "sc_qmm_bf16",
     "sc_qmm_bf16_path",
+    "sc_qmm_bf16_noalloc",
     "sc_vocab_gather_bf16",
     "sc_qembed_gather_bf16",
     "sc_dequantize_bf16",
@@ -76,6 +77,8 @@ def load():
         lib.sc_qmm_bf16.restype = i32
         lib.sc_qmm_bf16_path.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, i32, p]
         lib.sc_qmm_bf16_path.restype = i32
+        lib.sc_qmm_bf16_noalloc.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
+        lib.sc_qmm_bf16_noalloc.restype = i32
         lib.sc_vocab_gather_bf16.argtypes = [p, i32, i64, p, i64, i64, i64, p, p]
         lib.sc_vocab_gather_bf16.restype = i32
         lib.sc_qembed_gather_bf16.argtypes = [p, i32, i64, p, p, p, i64, i64, i64, i32, i32, p, p]
@@ -162,8 +165,11 @@ def _bf16(t, name):
     return t
 
 
-def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO, out=None):
-    """y = bf16(x @ dequant(wq, scales, biases)^T) (+ bias), x [..., K] -> [..., N]."""
+def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO, out=None, no_alloc=False):
+    """y = bf16(x @ dequant(wq, scales, biases)^T) (+ bias), x [..., K] -> [..., N].
+
+    ``no_alloc``: call ``sc_qmm_bf16_noalloc`` (the library allocates nothing;
+    pass ``out`` too for a call that allocates nothing at all)."""
     lib = load()
     _require_gpu(x, wq, scales, biases, bias)
     _bf16(x, "x"), _bf16(scales, "scales"), _bf16(biases, "biases")
@@ -193,8 +199,14 @@ def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO,
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         ev0.record()
-    rc = lib.sc_qmm_bf16_path(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),
-                              M, N, K, bits, group_size, path, st)
+    if no_alloc:
+        if path != PATH_AUTO:
+            raise ValueError("the allocation-free entry point chooses its kernel itself (path must be AUTO)")
+        rc = lib.sc_qmm_bf16_noalloc(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),
+                                     M, N, K, bits, group_size, st)
+    else:
+        rc = lib.sc_qmm_bf16_path(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),
+                                  M, N, K, bits, group_size, path, st)
     if sink is not None:
         ev1.record()
         sink.append((ev0, ev1, M, N, K, bits))

@@ -17,7 +17,7 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
                      const DmaFused *fused = nullptr);
 bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K);
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc);
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -151,7 +151,7 @@ static int check_qmm(const void *x, const void *wq, const void *s, const void *b
 
 static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
-                        int group_size, void *stream, int path) {
+                        int group_size, void *stream, int path, bool no_alloc = false) {
     int rc = check_qmm(x, wq, s, b, y, M, N, K, bits, group_size);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -162,7 +162,7 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         // takes the 32-column generic-K kernel; x that fits no LDS layout, the GEMM
         rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         if (rc != SC_EUNSUPPORTED) return rc;
-        rc = launch_qgemv16(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        rc = launch_qgemv16(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc);
         if (rc != SC_EUNSUPPORTED) return rc;
         rc = launch_qgemv_skinny(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         if (rc != SC_EUNSUPPORTED) return rc;
@@ -265,6 +265,13 @@ int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scal
                      const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
                      int group_size, int path, void *hip_stream) {
     return qmm_dispatch(x, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream, path);
+}
+
+int sc_qmm_bf16_noalloc(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                        const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                        int group_size, void *hip_stream) {
+    return qmm_dispatch(x, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream,
+                        SC_QMM_PATH_AUTO, /*no_alloc=*/true);
 }
 
 int sc_vocab_gather_bf16(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,

@@ -27,7 +27,10 @@
 //   (deterministic, no cross-workgroup fences).
 // Nothing dequantized is written to memory: HBM traffic is packed weights,
 // scales, biases, x and y (+ the small partials of split tiles).
+#include <mutex>
+
 #include "sc_common.h"
+#include "../../include/shardcompute_hip.h"
 
 namespace sc {
 
@@ -324,6 +327,35 @@ __global__ void __launch_bounds__(256) qgemv_finalize_kernel(const float *partia
 
 // ---------------------------------------------------------------- host side
 
+// Split-K partials of the allocation-free entry point (sc_qmm_bf16_noalloc): a
+// file-scope device array, one copy per GPU, held until the process ends.  Its
+// device address is looked up once per device (hipGetSymbolAddress, with that
+// device current) and kept; host code passes only that address to kernels.
+// Every entry a split-K launch reads is written by the same launch first, so no
+// part of it needs clearing between calls.
+static __device__ __align__(256) float scratch[SC_QMM_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+static constexpr int kScratchDevices = 64;
+static float *g_scratch_ptr[kScratchDevices];
+static std::mutex g_scratch_mu;
+
+static int noalloc_scratch(float **out) {
+    int dev = 0;
+    SC_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kScratchDevices) return set_error(SC_EINVAL, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(SC_ELAUNCH, "qmm_noalloc: hipGetSymbolAddress of the scratch array failed on device "
+                                         "%d: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return SC_OK;
+}
+
 struct Gemv16Plan {
     int splits, spans_per_split, waves, lds;
 };
@@ -379,8 +411,10 @@ static int launch_gemv16_t(const Gemv16Args &a, const Gemv16Plan &p, hipStream_t
 }
 
 // Returns SC_EUNSUPPORTED when the shape does not suit this kernel (caller falls back).
+// no_alloc: the split-K partials go to the file-scope scratch array (shapes that
+// need more than it holds are rejected) instead of the library-owned buffer.
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream) {
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc) {
     if (M < 1 || M > 32) return SC_EUNSUPPORTED;
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16)) return SC_EUNSUPPORTED;
     Gemv16Plan p;
@@ -390,10 +424,21 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y; a.partials = nullptr;
     a.M = M; a.N = N; a.K = K; a.G = K / 64; a.spans_per_split = p.spans_per_split;
     if (p.splits > 1) {
-        SplitKScratch ws;
-        const int rc = splitk_scratch((size_t)p.splits * M * N, 1, &ws);
-        if (rc) return rc;
-        a.partials = ws.partials;
+        const size_t need = (size_t)p.splits * M * N;
+        if (no_alloc) {
+            constexpr size_t cap = SC_QMM_NOALLOC_SCRATCH_BYTES / sizeof(float);
+            if (need > cap)
+                return set_error(SC_EINVAL, "qmm_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K scratch, above "
+                                            "the %zu-byte maximum", M, N, K, need * sizeof(float),
+                                 (size_t)SC_QMM_NOALLOC_SCRATCH_BYTES);
+            const int rc = noalloc_scratch(&a.partials);
+            if (rc) return rc;
+        } else {
+            SplitKScratch ws;
+            const int rc = splitk_scratch(need, 1, &ws);
+            if (rc) return rc;
+            a.partials = ws.partials;
+        }
     }
     int rc;
     const int mrows = M <= 8 ? 8 : M <= 16 ? 16 : 32;
