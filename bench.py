@@ -33,7 +33,14 @@ Printed (one JSON line on stdout):
   projections plus 1/32 of the lm_head rows at M = batch, repeated for ~10 s,
   scaled to tokens/s of the 32-layer model's linear layers;
 * ``prefill.qgemm_roofline``: the prefill quantized GEMM at M = prompt tokens on
-  layer 0's four projection shapes, TFLOP/s against 2.5 PFLOP/s dense bf16.
+  layer 0's four projection shapes, TFLOP/s against 2.5 PFLOP/s dense bf16;
+* ``other_configs``: the other workloads of the path, each beside the headline:
+  the vocab-sharded gather of 64 x 2048 Zipf(1.1) ids on rank 0 of a 2-way split
+  of the 128256 x 4096 table (GB/s on ids + written rows + unique in-shard rows
+  read) and that configuration's W4 lm_head at M = 64; batch-16 decode of the
+  headline model; the batch-1 decode qGEMV at 8 bits; TinyLlama-shape W4
+  decode (32-token prompt, batch 1); and the Llama-3-70B rank-0-of-8 shard at
+  batch 32 after a 1024-token prefill, W4 and W8 (all-reduces as identity).
 """
 import argparse
 import asyncio
@@ -53,6 +60,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "qgemv_m1_w4_llama3_8b_decode_traf
 TRUNK_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_step_w4_llama3_8b_traffic.json")
 
 LLAMA3_8B = dict(vocab=128256, hidden=4096, inter=14336, layers=32, heads=32, kv_heads=8, theta=500000.0, eps=1e-5)
+TINYLLAMA = dict(vocab=32000, hidden=2048, inter=5632, layers=22, heads=32, kv_heads=4, theta=10000.0, eps=1e-5)
+LLAMA3_70B = dict(vocab=128256, hidden=8192, inter=28672, layers=80, heads=64, kv_heads=8, theta=500000.0, eps=1e-5)
 
 
 def log(*a):
@@ -75,25 +84,39 @@ def parse_args():
                    help="build the weights and run only the per-launch GEMV pass (for counter profiling)")
     p.add_argument("--trunk-only", action="store_true",
                    help="prefill, then only eager whole-trunk decode launches (for counter profiling)")
+    p.add_argument("--trunk-timeline", action="store_true",
+                   help="prefill, then print the whole-trunk launch's per-op timeline (JSON) and exit")
+    p.add_argument("--no-extras", dest="extras", action="store_false",
+                   help="skip the other configurations' measurements (gather, lm_head, batch 16, W8, ...)")
+    p.add_argument("--no-extra-models", dest="extras_models", action="store_false",
+                   help="skip the extra model builds (W8 GEMV, TinyLlama, 70B shard)")
     return p.parse_args()
 
 
 # ---------------------------------------------------------------- model
 
 
-def build_model(cfg, layers, bits, capacity, seed=0):
+def build_model(cfg, layers, bits, capacity, seed=0, world_size=1, rank=0):
+    """Random-init quantized decoder of shape ``cfg``; with world_size > 1, rank
+    ``rank``'s shard (local heads, intermediate and vocab rows), its collectives
+    the identity."""
     import torch
     from shardcompute_amd import _lib
+    from shardcompute_amd.communicator import IdentityCommunicator
     from shardcompute_amd.parallel.transformer import ParallelTransformer
     dev = torch.device("cuda", 0)
+    ws = world_size
     H, I, V = cfg["hidden"], cfg["inter"], cfg["vocab"]
     D = H // cfg["heads"]
-    nq, nkv = cfg["heads"] * D, cfg["kv_heads"] * D
-    m = ParallelTransformer(vocab_size=V, hidden_size=H, num_layers=layers, num_heads=cfg["heads"],
-                            intermediate_size=I, world_size=1, rank=0, num_kv_heads=cfg["kv_heads"],
-                            max_position_embeddings=capacity, rms_norm_eps=cfg["eps"], rope_base=cfg["theta"],
-                            use_quantized=True, quantization_bits=bits, quantization_group_size=64,
-                            embedding="vocab", quantized_lm_head=True, device=dev)
+    nq, nkv = cfg["heads"] // ws * D, cfg["kv_heads"] // ws * D
+    I, V = I // ws, V // ws
+    comm = IdentityCommunicator(rank, ws) if ws > 1 else None
+    m = ParallelTransformer(vocab_size=cfg["vocab"], hidden_size=H, num_layers=layers, num_heads=cfg["heads"],
+                            intermediate_size=cfg["inter"], world_size=ws, rank=rank, communicator=comm,
+                            num_kv_heads=cfg["kv_heads"], max_position_embeddings=capacity,
+                            rms_norm_eps=cfg["eps"], rope_base=cfg["theta"], use_quantized=True,
+                            quantization_bits=bits, quantization_group_size=64, embedding="vocab",
+                            quantized_lm_head=True, device=dev)
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
 
@@ -339,6 +362,25 @@ def eager_gemv_passes(model, batch, bits, passes):
 # ---------------------------------------------------------------- CPU baseline
 
 
+def host_cpu():
+    """Cores this process may run on and the CPU model name (from /proc/cpuinfo)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"affinity_cores": n, "model": model}
+
+
+
 def cpu_baseline(model, batch, bits, seconds):
     """The C restatement on decoder layer 0's projections + 1/32 of the lm_head rows."""
     import numpy as np
@@ -376,12 +418,197 @@ def cpu_baseline(model, batch, bits, seconds):
         t_lm += t2 - t1
         reps += 1
     per_token = model.num_layers * t_layer / reps + 32 * t_lm / reps
+    host = host_cpu()
     return {"value": round(batch / per_token, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+            "host_cores": host["affinity_cores"], "cpu_model": host["model"],
+            "threads_note": (f"OpenMP threads = min(affinity cores, 16): {threads} of the "
+                             f"{host['affinity_cores']} cores this process may run on"),
             "sample": (f"oracle C restatement (fp64 accumulate, OpenMP) of the W{bits} g64 quantized matmuls: "
                        f"decoder layer 0's q|k|v, o, gate|up, down plus lm_head rows [0, {rows}) at M={batch}, "
                        f"{reps} repetitions in {time.perf_counter() - t_start:.1f} s, scaled x{model.num_layers} "
                        f"layers and x32 lm_head rows; attention and norms not included")}
 
+
+
+# ---------------------------------------------------------------- further workloads
+#
+# The other configurations of the measured hot path, each reported beside the
+# headline (never required: a failure is logged and reported as an error string).
+
+
+def _events_us(fn, reps, warm=2):
+    """Average duration of fn() over ``reps`` back-to-back calls: HIP events on the
+    current stream (the stream the library launches on)."""
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
+def zipf_ids(n_vocab, shape, s=1.1, seed=0):
+    """Token ids from the bounded Zipf law p(k) ~ k^-s, k = 1..n_vocab, id = k - 1."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    p = np.arange(1, n_vocab + 1, dtype=np.float64) ** -s
+    p /= p.sum()
+    return rng.choice(n_vocab, size=shape, p=p).astype(np.int64)
+
+
+def bench_vocab_gather(reps=20):
+    """Rank 0 of a world_size-2 vocab split of a 128256 x 4096 bf16 table (rows
+    [0, 64128)), ids [64, 2048] Zipf(1.1) over the whole vocabulary: the masked
+    gather, GB/s on the algorithmic bytes ids + written rows + unique in-shard
+    rows read."""
+    import numpy as np
+    import torch
+    from shardcompute_amd import _lib
+    V, VL, D = 128256, 64128, 4096
+    ids_np = zipf_ids(V, (64, 2048))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    table = torch.randn((VL, D), generator=g, device="cuda").mul_(0.02).to(torch.bfloat16)
+    ids = torch.from_numpy(ids_np).cuda()
+    out = torch.empty((64, 2048, D), dtype=torch.bfloat16, device="cuda")
+    us = _events_us(lambda: _lib.vocab_gather(ids, table, 0, out=out), reps)
+    T = ids_np.size
+    inshard = ids_np[ids_np < VL]
+    U = int(np.unique(inshard).size)
+    nbytes = T * 8 + T * D * 2 + U * D * 2
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {"kernel": "vocab_gather_kernel", "ids": [64, 2048], "table": [VL, D], "vocab": V,
+           "in_shard_frac": round(inshard.size / T, 4), "unique_in_shard_rows": U, "bytes": int(nbytes),
+           "avg_us": round(us, 2), "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    log(f"vocab gather (config 3): {us:.1f} us, {gbs:.0f} GB/s, U={U}")
+    del table, ids, out
+    return res
+
+
+def bench_lm_head_m64(reps=10):
+    """The config-3 quantized lm_head: W4 g64 [64128, 4096] on hidden [64, 4096]."""
+    import torch
+    from shardcompute_amd import _lib
+    N, K, M = 64128, 4096, 64
+    g = torch.Generator(device="cuda")
+    g.manual_seed(4)
+    wq, s, b = _lib.quantize(torch.randn((N, K), generator=g, device="cuda").mul_(0.02), bits=4)
+    x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    us = _events_us(lambda: _lib.qmm(x, wq, s, b, bits=4, out=y), reps)
+    nbytes = qmm_bytes(M, N, K, 4)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    log(f"lm_head M=64 (config 3): {us:.1f} us, {gbs:.0f} GB/s, {tf:.0f} TFLOP/s")
+    del wq, s, b, x, y
+    return {"M": M, "N": N, "K": K, "bits": 4, "bytes": int(nbytes), "avg_us": round(us, 2), "GBs": round(gbs, 1),
+            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 1)}
+
+
+def bench_w8_gemv(reps):
+    """Batch-1 decode qGEMV at 8 bits on the Llama-3-8B projection shapes (4 layers'
+    distinct weights + the lm_head, more than the 256 MB last-level cache)."""
+    import torch
+    model = build_model(LLAMA3_8B, 4, 8, 64, seed=5)
+    g = time_gemv_launches(model, 1, 8, reps)
+    del model
+    torch.cuda.empty_cache()
+    return {"kernel": "qgemv_m1_kernel<8, *, *>", "avg_launch_us": round(g["avg_us"], 3),
+            "bytes_per_launch": round(g["bytes_per_launch"]), "GBs": round(g["GBs"], 1),
+            "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "per_shape": g["per_shape"]}
+
+
+def decode_run(model, B, prompt, steps, warm=8, seed=1):
+    """Prefill B random prompts of ``prompt`` tokens, then greedy decode: returns
+    (prefill seconds, decode tokens/s over ``steps`` timed steps, ms per step,
+    whether the whole-trunk plan ran)."""
+    import torch
+    from shardcompute_amd import _lib
+    from shardcompute_amd.executor import DecodeGraph
+    cap = prompt + warm + steps + 8
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    ids = torch.randint(0, model.vocab_size, (B, prompt), generator=gen, device="cuda", dtype=torch.int64)
+    cache = model.new_cache(B, cap)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits, _ = asyncio.run(model.forward(ids, past_key_values=cache, use_cache=True, last_only=True))
+    torch.cuda.synchronize()
+    pre_s = time.perf_counter() - t0
+    tokens = torch.zeros((B, warm + steps + 2), dtype=torch.int32, device="cuda")
+    dec = DecodeGraph(model, cache, tokens)
+    _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
+    _lib.add_i32(cache.counters[1:], 1, n=1)
+    dec.run(1)
+    dec.run(warm)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dec.run(steps)
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    trunk = dec.bufs.plan is not None
+    if trunk and dec.bufs.plan.status() != 0:
+        raise RuntimeError("whole-trunk launch gave up waiting")
+    del dec, cache, tokens, logits
+    return pre_s, B * steps / el, el / steps * 1e3, trunk
+
+
+def bench_decode_config(name, cfg, bits, B, prompt, steps, layers=None, world_size=1):
+    import torch
+    L = layers or cfg["layers"]
+    t0 = time.perf_counter()
+    model = build_model(cfg, L, bits, prompt + steps + 32, seed=7, world_size=world_size)
+    build_s = time.perf_counter() - t0
+    pre_s, tok_s, ms, trunk = decode_run(model, B, prompt, steps)
+    log(f"{name}: built in {build_s:.1f} s, prefill {B}x{prompt} in {pre_s * 1e3:.0f} ms, decode {tok_s:.1f} tok/s "
+        f"({ms:.3f} ms/step, {'whole-trunk' if trunk else 'per-op'} path)")
+    res = {"layers": L, "bits": bits, "batch": B, "prefill_tokens": prompt, "steps": steps,
+           "world_size": world_size, "rank": 0, "tok_s": round(tok_s, 1), "ms_per_step": round(ms, 4),
+           "prefill_ms": round(pre_s * 1e3, 1), "path": "whole-trunk launch" if trunk else "per-op launches"}
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_batch16(model, steps):
+    """Batch-16 greedy decode of the headline model after a 2048-token prefill per sequence."""
+    pre_s, tok_s, ms, trunk = decode_run(model, 16, 2048, steps)
+    log(f"8B batch 16: prefill 16x2048 in {pre_s * 1e3:.0f} ms, decode {tok_s:.1f} tok/s ({ms:.3f} ms/step)")
+    return {"batch": 16, "prefill_tokens": 2048, "steps": steps, "tok_s": round(tok_s, 1),
+            "ms_per_step": round(ms, 4), "prefill_ms": round(pre_s * 1e3, 1), "path": "per-op launches"}
+
+
+def run_extras(model, args):
+    import torch
+    out = {}
+    jobs = [
+        ("vocab_gather_config3", lambda: bench_vocab_gather()),
+        ("lm_head_m64_config3", lambda: bench_lm_head_m64()),
+        ("batch16_llama3_8b_w4", lambda: bench_batch16(model, 32)),
+    ]
+    if args.extras_models:
+        jobs += [
+            ("w8_decode_gemv_llama3_8b", lambda: bench_w8_gemv(args.kernel_reps)),
+            ("tinyllama_w4_bs1", lambda: bench_decode_config("TinyLlama W4 bs1", TINYLLAMA, 4, 1, 32, 128)),
+            ("llama3_70b_rank0_of_8_w4_bs32", lambda: bench_decode_config(
+                "70B rank-0 shard W4 bs32", LLAMA3_70B, 4, 32, 1024, 32, world_size=8)),
+            ("llama3_70b_rank0_of_8_w8_bs32", lambda: bench_decode_config(
+                "70B rank-0 shard W8 bs32", LLAMA3_70B, 8, 32, 1024, 32, world_size=8)),
+        ]
+    for name, fn in jobs:
+        try:
+            out[name] = fn()
+        except Exception as e:           # reported, never required
+            log(f"{name}: failed: {e!r}")
+            out[name] = {"error": repr(e)[:300]}
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 # ---------------------------------------------------------------- main
 
@@ -432,6 +659,24 @@ def main():
 
     tokens = torch.zeros((B, W + K + 2), dtype=torch.int32, device="cuda")
     dec = DecodeGraph(model, cache, tokens)
+    if args.trunk_timeline:
+        if dec.bufs.plan is None:
+            log("trunk-timeline: the whole-trunk plan does not apply to this configuration")
+            sys.exit(2)
+        _lib.argmax(logits.reshape(B, -1), ids=dec.bufs.ids.view(-1), tokens=tokens, step=cache.counters[1:])
+        _lib.add_i32(cache.counters[1:], 1, n=1)
+        dec.run(1 + W)                  # eager step, capture, warm graph replays
+        plan = dec.bufs.plan
+        plan.trace(True)
+        t_us = time_trunk_launches(dec, args.kernel_reps)
+        tl = plan.timeline()
+        plan.trace(False)
+        tl.update({"workload": f"Llama-3-8B-shape W{args.bits}g64 whole-trunk decode launch, batch 1, context "
+                               f"{cache.length}", "layers": args.layers, "avg_launch_us": round(t_us, 1),
+                   "stamps": "s_memrealtime (100 MHz) by each workgroup's control wave, last of "
+                             f"{args.kernel_reps + 1} back-to-back launches"})
+        print(json.dumps(tl), flush=True)
+        return
     if args.trunk_only:
         if dec.bufs.plan is None:
             log("trunk-only: the whole-trunk plan does not apply to this configuration")
@@ -499,6 +744,8 @@ def main():
         except Exception as e:       # the baseline is reported, never required
             log(f"cpu baseline unavailable: {e}")
 
+    extras = run_extras(model, args) if args.extras and B == 1 and args.layers == 32 else None
+
     kv_bytes = 2 * args.layers * B * cfg["kv_heads"] * (cfg["hidden"] // cfg["heads"]) * 2 * (P + W + K // 2)
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": K, "warmup": W,
@@ -522,6 +769,7 @@ def main():
                                                / HBM_PEAK_GBS, 4)},
         "gemv_per_shape": g["per_shape"],
         "first_tokens": first,
+        "other_configs": extras,
     }
     print(json.dumps(line), flush=True)
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 8
+#define SC_ABI_VERSION 9
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -357,6 +357,22 @@ int sc_decode_plan_create(const sc_decode_model *model, const sc_decode_layer *l
 int sc_decode_plan_run(void *plan, void *hip_stream);
 int sc_decode_plan_status(void *plan, uint32_t *status);
 void sc_decode_plan_destroy(void *plan);
+
+/*
+ * Per-op timeline of the whole-trunk launch: the fused counterpart of the per-layer
+ * timing of ParallelExecutor.forward_with_timing (src/shardcompute/worker/executor.py:
+ * 155-227), which cannot bracket layers inside one launch with host clocks.
+ * sc_decode_plan_trace(plan, 1) allocates a stamp buffer (not under stream capture)
+ * and makes later launches record, per workgroup w and op j (op 0 the embedding,
+ * then 6 per layer: q|k|v, attention, key-range merge, o, gate|up, down), the
+ * 100 MHz real-time clock at four points: the op's items all computed (k = 0), its
+ * output published (1), its input polled (2) and staged (3), at
+ * stamps[(w * ops + j) * 4 + k]; (plan, 0) frees it.  sc_decode_plan_read_trace
+ * copies the last launch's stamps (n entries at least workgroups * ops * 4;
+ * stamps may be null to query the sizes), synchronously.
+ */
+int sc_decode_plan_trace(void *plan, int enable);
+int sc_decode_plan_read_trace(void *plan, uint32_t *stamps, int64_t n, int *workgroups, int *ops);
 
 #ifdef __cplusplus
 }

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -45,6 +45,8 @@ EXPORTS = (
     "sc_decode_plan_run",
     "sc_decode_plan_status",
     "sc_decode_plan_destroy",
+    "sc_decode_plan_trace",
+    "sc_decode_plan_read_trace",
 )
 
 _lib = None
@@ -124,6 +126,10 @@ def load():
         lib.sc_decode_plan_status.restype = i32
         lib.sc_decode_plan_destroy.argtypes = [p]
         lib.sc_decode_plan_destroy.restype = None
+        lib.sc_decode_plan_trace.argtypes = [p, i32]
+        lib.sc_decode_plan_trace.restype = i32
+        lib.sc_decode_plan_read_trace.argtypes = [p, p, i64, p, p]
+        lib.sc_decode_plan_read_trace.restype = i32
         v = lib.sc_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"libshardcompute_hip ABI {v}, expected {ABI_VERSION}")

@@ -54,6 +54,8 @@ int launch_add_i32(int32_t *p, long n, int32_t delta, hipStream_t stream);
 int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, void **out);
 int decode_plan_run(void *plan, hipStream_t stream);
 int decode_plan_status(void *plan, unsigned *status);
+int decode_plan_trace(void *plan, int enable);
+int decode_plan_read_trace(void *plan, uint32_t *host, int64_t n, int *P, int *nops);
 void decode_plan_destroy(void *plan);
 
 constexpr int PRO_NORM_KIND = 1;
@@ -390,6 +392,12 @@ int sc_decode_plan_run(void *plan, void *hip_stream) {
 }
 
 int sc_decode_plan_status(void *plan, uint32_t *status) { return decode_plan_status(plan, status); }
+
+int sc_decode_plan_trace(void *plan, int enable) { return decode_plan_trace(plan, enable); }
+
+int sc_decode_plan_read_trace(void *plan, uint32_t *stamps, int64_t n, int *workgroups, int *ops) {
+    return decode_plan_read_trace(plan, stamps, n, workgroups, ops);
+}
 
 void sc_decode_plan_destroy(void *plan) { decode_plan_destroy(plan); }
 

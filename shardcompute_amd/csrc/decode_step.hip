@@ -105,6 +105,7 @@ struct Args {
     // LDS layout (byte offsets into dynamic shared memory)
     int n_items;            // attention items per unit at most (keys per unit / 8)
     int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
+    uint32_t *trace;          // null, or [P][nops][4] real-time stamps of the last launch
 };
 
 __device__ __forceinline__ void ll_store(uint2 *p, uint32_t data, uint32_t ep) {
@@ -434,6 +435,13 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     };
 
     auto epoch = [&](int j) -> uint32_t { return base * (uint32_t)nops + (uint32_t)j + 1u; };
+    // Op timeline (when the plan traces): per (workgroup, op) the 100 MHz real-time
+    // clock when the op's items were all computed (0), its output published (1), its
+    // input polled (2) and staged (3); the control wave stamps them.
+    auto stamp = [&](int j, int k) __attribute__((always_inline)) {
+        if (a.trace && lane == 0 && j >= 0 && j < nops)
+            a.trace[((size_t)wg * nops + j) * 4 + k] = (uint32_t)__builtin_amdgcn_s_memrealtime();
+    };
     auto kind_of = [&](int j) -> int { return j == 0 ? -1 : (j - 1) % NT; };
 
     // is_ctl: std::true_type in the control wave's copy, std::false_type in the
@@ -442,6 +450,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         constexpr bool ctl = decltype(is_ctl)::value;
         __syncthreads();                                             // B1: op jj - 1 computed
         const int jp = jj - 1;
+        if (ctl) stamp(jp, 0);
         // ------------------------------------------------------------ finish op jp
         if (jp >= 0 && !s_abort) {
             const int kp = kind_of(jp);
@@ -551,6 +560,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 }
             }
         }
+        if (ctl) stamp(jp, 1);
         if (jj >= nops) return;
         // ------------------------------------------------------------ stage op jj
         const int k = kind_of(jj);
@@ -700,6 +710,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             }
             if (!ok && lane == 0) s_abort = 1;
         }
+        if (ctl) stamp(jj, 2);
         __syncthreads();                                             // B2: raw input staged
         if (s_abort) {
             __syncthreads();
@@ -726,6 +737,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             }
         }
         __syncthreads();                                             // B3: op jj's input ready
+        if (ctl) stamp(jj, 3);
     };
 
     // ====================================================================== item stream
@@ -1073,6 +1085,7 @@ struct DecodePlan {
     Args args{};
     LayerPtrs *d_layers = nullptr;
     void *d_mem = nullptr;      // exchange buffers, epoch base, status
+    uint32_t *d_trace = nullptr;  // op timeline (allocated while tracing)
     size_t lds = 0;
 };
 
@@ -1259,9 +1272,39 @@ int decode_plan_status(void *plan, unsigned *status) {
     return SC_OK;
 }
 
+int decode_plan_trace(void *plan, int enable) {
+    DecodePlan *pl = static_cast<DecodePlan *>(plan);
+    if (!pl) return set_error(SC_EINVAL, "decode_plan_trace: null plan");
+    const size_t bytes = (size_t)pl->P * pl->args.nops * 4 * sizeof(uint32_t);
+    if (enable && !pl->d_trace) {
+        SC_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&pl->d_trace), bytes));
+        SC_HIP_CHECK(hipMemset(pl->d_trace, 0, bytes));
+    } else if (!enable && pl->d_trace) {
+        SC_HIP_CHECK(hipDeviceSynchronize());
+        SC_HIP_CHECK(hipFree(pl->d_trace));
+        pl->d_trace = nullptr;
+    }
+    pl->args.trace = pl->d_trace;
+    return SC_OK;
+}
+
+int decode_plan_read_trace(void *plan, uint32_t *host, int64_t n, int *P, int *nops) {
+    DecodePlan *pl = static_cast<DecodePlan *>(plan);
+    if (!pl || !P || !nops) return set_error(SC_EINVAL, "decode_plan_read_trace: null argument");
+    *P = pl->P;
+    *nops = pl->args.nops;
+    if (!host) return SC_OK;
+    if (!pl->d_trace) return set_error(SC_EINVAL, "decode_plan_read_trace: tracing is not enabled");
+    const int64_t need = (int64_t)pl->P * pl->args.nops * 4;
+    if (n < need) return set_error(SC_EINVAL, "decode_plan_read_trace: %lld entries needed", (long long)need);
+    SC_HIP_CHECK(hipMemcpy(host, pl->d_trace, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    return SC_OK;
+}
+
 void decode_plan_destroy(void *plan) {
     DecodePlan *pl = static_cast<DecodePlan *>(plan);
     if (!pl) return;
+    if (pl->d_trace) (void)hipFree(pl->d_trace);
     (void)hipFree(pl->d_layers);
     (void)hipFree(pl->d_mem);
     delete pl;

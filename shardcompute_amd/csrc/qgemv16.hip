@@ -21,8 +21,10 @@
 //       acc += s * P + (b - off * s) * xsum[m, g]    (off = 128 W4, 0 W8)
 //   with xsum[m, g] the sum of x over the group (computed at staging).  Rows of
 //   x beyond M are zero operands; their outputs are never written.
-// * Waves of a workgroup split K; their tiles are reduced through LDS.  When a
-//   column tile is also split across workgroups (gridDim.y > 1), each writes an
+// * A workgroup stages x for its K range (split) once and owns tiles_per_wg
+//   consecutive 16-column tiles; each wave computes whole tiles over that range
+//   (chunks in order), streaming its (tile, chunk) items with the next one in
+//   flight.  When K is split across workgroups (gridDim.y > 1), each writes an
 //   fp32 partial tile and a second kernel sums the partials in split order
 //   (deterministic, no cross-workgroup fences).
 // Nothing dequantized is written to memory: HBM traffic is packed weights,
@@ -44,6 +46,7 @@ struct Gemv16Args {
     float *partials;       // [splits, M, N] when gridDim.y > 1
     int M, N, K, G;
     int spans_per_split;   // multiple of CHUNK_SPANS
+    int tiles_per_wg;      // 16-column tiles of one workgroup (its waves take them in turn)
 };
 
 typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4v;
@@ -98,7 +101,6 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     const int nwaves = blockDim.x >> 6;
     const int j = lane & 15;          // column within the tile / A row index
     const int q = lane >> 4;          // lane-group
-    const int n0 = blockIdx.x * 16;
     const int split = blockIdx.y;
     const int M = a.M, N = a.N;
 
@@ -115,10 +117,12 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
     float *xs = reinterpret_cast<float *>(smem + (size_t)M * xstride * 16);
 
-    const int n = min(n0 + j, N - 1);
-    const uint4 *wrow = reinterpret_cast<const uint4 *>(a.wq) + (size_t)n * ((size_t)a.K * BITS / 128);
-    const uint16_t *srow = a.s + (size_t)n * a.G;
-    const uint16_t *brow = a.b + (size_t)n * a.G;
+    // this wave's items: (tile, chunk) for its tiles wave, wave + nwaves, ... of the
+    // workgroup, every chunk of the split in order
+    const int ntiles = (N + 15) / 16;
+    const int tile0 = blockIdx.x * a.tiles_per_wg;
+    const int my_tiles = max(0, (min(a.tiles_per_wg, ntiles - tile0) - wave + nwaves - 1) / nwaves);
+    const int nitems = my_tiles * nchunks;
 
     // ---- 1. x words for LDS (first round issued before any weight load)
     constexpr int XR = 4;   // x words held per thread per round
@@ -150,7 +154,13 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     // ---- 2. first chunk of weights + scales/biases
     uint4 wA[CHUNK_SPANS], wB[CHUNK_SPANS];
     uint4 sA, bA, sB, bB;   // W4: 8 groups (uint4); W8: 4 groups in .x/.y
-    auto w_issue = [&](int c, uint4 *w, uint4 &sv, uint4 &bv) {
+    // item it of this wave: chunk it % nchunks of tile tile0 + wave + nwaves * (it / nchunks)
+    auto w_issue = [&](int it, uint4 *w, uint4 &sv, uint4 &bv) {
+        const int ti = it / nchunks, c = it - ti * nchunks;
+        const int n = min((tile0 + wave + nwaves * ti) * 16 + j, N - 1);
+        const uint4 *wrow = reinterpret_cast<const uint4 *>(a.wq) + (size_t)n * ((size_t)a.K * BITS / 128);
+        const uint16_t *srow = a.s + (size_t)n * a.G;
+        const uint16_t *brow = a.b + (size_t)n * a.G;
         const int sp0 = sp_begin + c * CHUNK_SPANS;
 #pragma unroll
         for (int t = 0; t < CHUNK_SPANS; ++t) w[t] = wrow[(size_t)(sp0 + t) * 4 + q];
@@ -165,8 +175,7 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
             bv = make_uint4(b2.x, b2.y, 0u, 0u);
         }
     };
-    int c = wave;
-    if (c < nchunks) w_issue(c, wA, sA, bA);
+    if (nitems > 0) w_issue(0, wA, sA, bA);
 
     // ---- 3. stage x (remaining rounds wait for everything; only large M*K needs them)
     x_store(0);
@@ -257,58 +266,56 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
         }
     };
 
-    while (c < nchunks) {
-        const int cn = c + nwaves;
-        if (cn < nchunks) w_issue(cn, wB, sB, bB);
-        compute_chunk(c, wA, sA, bA);
-        c = cn;
-        if (c >= nchunks) break;
-        const int cn2 = c + nwaves;
-        if (cn2 < nchunks) w_issue(cn2, wA, sA, bA);
-        compute_chunk(c, wB, sB, bB);
-        c = cn2;
-    }
-
-    // ---- 5. combine group parities: final value of (m, column j) per lane
+    // ---- 5. per finished tile: combine the group parities (final value of (m, column
+    // j) per lane: W4 (MROWS <= 8) m = 4q + r in lane-groups q < 2, else m = 16h + 4q + r)
+    // and write the tile (or its partial over this split)
     constexpr int NOUT = (BITS == 4) ? (MROWS <= 8 ? 1 : C::NSETS / 2) : C::NSETS;
-    f32x4v fin[NOUT];
-    if (BITS == 4 && MROWS <= 8) {
+    auto finish_tile = [&](int ti) {
+        f32x4v fin[NOUT];
+        if (BITS == 4 && MROWS <= 8) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) fin[0][r] = acc[0][r] + __shfl_xor(acc[0][r], 32);
-    } else if (BITS == 4) {
+            for (int r = 0; r < 4; ++r) fin[0][r] = acc[0][r] + __shfl_xor(acc[0][r], 32);
+        } else if (BITS == 4) {
 #pragma unroll
-        for (int h = 0; h < NOUT; ++h) fin[h] = acc[h] + acc[h + NOUT];
-    } else {
-#pragma unroll
-        for (int h = 0; h < NOUT; ++h) fin[h] = acc[h];
-    }
-    // m of fin[h][r] in lane-group q: W4 (MROWS<=8): 4q + r for q < 2; otherwise 16h + 4q + r
-    // ---- 6. reduce the waves through LDS: red[wave][m][16]
-    __syncthreads();
-    float *red = reinterpret_cast<float *>(smem);
-#pragma unroll
-    for (int h = 0; h < NOUT; ++h) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int m = (BITS == 4 && MROWS <= 8) ? 4 * q + r : 16 * h + 4 * q + r;
-            const bool keep = (BITS == 4 && MROWS <= 8) ? (q < 2) : true;
-            if (keep && m < M) red[(wave * M + m) * 16 + j] = fin[h][r];
-        }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < M * 16; idx += blockDim.x) {
-        const int m = idx >> 4, jj = idx & 15;
-        float v = 0.f;
-        for (int w = 0; w < nwaves; ++w) v += red[(w * M + m) * 16 + jj];
-        const int nn = n0 + jj;
-        if (nn >= N) continue;
-        if (gridDim.y == 1) {
-            uint32_t o = f2bf(v);
-            if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
-            a.y[(size_t)m * N + nn] = (uint16_t)o;
+            for (int h = 0; h < NOUT; ++h) fin[h] = acc[h] + acc[h + NOUT];
         } else {
-            a.partials[((size_t)split * M + m) * N + nn] = v;
+#pragma unroll
+            for (int h = 0; h < NOUT; ++h) fin[h] = acc[h];
         }
+        const int nn = (tile0 + wave + nwaves * ti) * 16 + j;
+        const bool keepq = (BITS == 4 && MROWS <= 8) ? (q < 2) : true;
+        if (nn < N && keepq) {
+#pragma unroll
+            for (int h = 0; h < NOUT; ++h) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = (BITS == 4 && MROWS <= 8) ? 4 * q + r : 16 * h + 4 * q + r;
+                    if (m < M) {
+                        const float v = fin[h][r];
+                        if (gridDim.y == 1) {
+                            uint32_t o = f2bf(v);
+                            if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
+                            a.y[(size_t)m * N + nn] = (uint16_t)o;
+                        } else {
+                            a.partials[((size_t)split * M + m) * N + nn] = v;
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < C::NSETS; ++s) acc[s] = f32x4v{0.f, 0.f, 0.f, 0.f};
+    };
+
+    // ---- 6. stream the items: the next one in flight while the current one computes
+    for (int it = 0; it < nitems; it += 2) {
+        if (it + 1 < nitems) w_issue(it + 1, wB, sB, bB);
+        compute_chunk(it % nchunks, wA, sA, bA);
+        if ((it + 1) % nchunks == 0) finish_tile(it / nchunks);
+        if (it + 1 >= nitems) break;
+        if (it + 2 < nitems) w_issue(it + 2, wA, sA, bA);
+        compute_chunk((it + 1) % nchunks, wB, sB, bB);
+        if ((it + 2) % nchunks == 0) finish_tile((it + 1) / nchunks);
     }
 }
 
@@ -357,42 +364,41 @@ static int noalloc_scratch(float **out) {
 }
 
 struct Gemv16Plan {
-    int splits, spans_per_split, waves, lds;
+    int splits, spans_per_split, waves, lds, tiles_per_wg, groups;
 };
 
+// Work is (tile, split) units of cps chunks each.  Splits: enough units for about
+// one per wave of a workgroup per CU, but no fewer than the x slice's LDS allows;
+// then ~one workgroup per CU per split, each owning a run of consecutive tiles.
 template <int BITS>
 static bool plan_gemv16(int M, int N, int K, Gemv16Plan *p) {
     using C = G16<BITS, 8>;
-    const int kGemvMaxWaves = gemv16_max_waves(M <= 8 ? 8 : 16);
+    const int maxw = gemv16_max_waves(M <= 8 ? 8 : 16);
     const DeviceInfo &di = device_info();
     const int tiles = (N + 15) / 16;
     const int chunk_k = CHUNK_SPANS * C::SPAN_K;
     if (K % chunk_k) return false;
     const int nchunks = K / chunk_k;
     const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
-    int splits = 1;
-    // enough workgroups for every CU, while each split keeps >= 2 chunks
-    while (tiles * splits < di.num_cus && nchunks / (splits * 2) >= 2) splits *= 2;
-    for (;;) {
-        const int cps = (nchunks + splits - 1) / splits;   // chunks per split
+    const int want = (di.num_cus * maxw + tiles - 1) / tiles;     // splits for one unit per wave
+    for (int s = want < 1 ? 1 : want; ; ++s) {
+        if (s > nchunks) s = nchunks;
+        const int cps = (nchunks + s - 1) / s;
         const int real = (nchunks + cps - 1) / cps;
-        const int spans = cps * CHUNK_SPANS;
-        const int kr = spans * C::SPAN_K;
-        int waves = cps < kGemvMaxWaves ? cps : kGemvMaxWaves;
-        // two chunks per wave when there are plenty of workgroups
-        if (tiles * real >= 2 * di.num_cus && waves > 1 && cps >= 2 * 4) waves = (cps + 1) / 2 < kGemvMaxWaves ? (cps + 1) / 2 : kGemvMaxWaves;
-        const int stage = M * (kr / 8 + 1) * 16 + M * (kr / 64) * 4;
-        const int red = waves * M * 16 * 4;
-        const int lds = stage > red ? stage : red;
+        const int kr = cps * chunk_k;
+        const int lds = M * (kr / 8 + 1) * 16 + M * (kr / 64) * 4;
         if (lds <= lds_cap) {
+            const int groups0 = (di.num_cus + real - 1) / real;
+            const int tpw = (tiles + groups0 - 1) / groups0;
             p->splits = real;
-            p->spans_per_split = spans;
-            p->waves = waves;
+            p->spans_per_split = cps * CHUNK_SPANS;
+            p->tiles_per_wg = tpw;
+            p->groups = (tiles + tpw - 1) / tpw;
+            p->waves = tpw < maxw ? tpw : maxw;
             p->lds = lds;
             return true;
         }
-        if (cps <= 1) return false;
-        splits *= 2;
+        if (s >= nchunks) return false;
     }
 }
 
@@ -405,7 +411,7 @@ static int launch_gemv16_t(const Gemv16Args &a, const Gemv16Plan &p, hipStream_t
                                          hipFuncAttributeMaxDynamicSharedMemorySize, p.lds));
         configured = p.lds;
     }
-    hipLaunchKernelGGL(kern, dim3((a.N + 15) / 16, p.splits), dim3(64 * p.waves), p.lds, stream, a);
+    hipLaunchKernelGGL(kern, dim3(p.groups, p.splits), dim3(64 * p.waves), p.lds, stream, a);
     SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
 }
@@ -423,6 +429,7 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     Gemv16Args a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y; a.partials = nullptr;
     a.M = M; a.N = N; a.K = K; a.G = K / 64; a.spans_per_split = p.spans_per_split;
+    a.tiles_per_wg = p.tiles_per_wg;
     if (p.splits > 1) {
         const size_t need = (size_t)p.splits * M * N;
         if (no_alloc) {

@@ -165,6 +165,64 @@ class TrunkPlan:
         _lib._check(lib.sc_decode_plan_status(self._handle, ctypes.byref(v)), "sc_decode_plan_status")
         return int(v.value)
 
+    # -------------------------------------------------------------- op timeline
+
+    OP_KINDS = ("qkv", "attn", "merge", "o", "gate_up", "down")
+
+    def trace(self, enable: bool = True):
+        """Make later launches record the per-op timeline (allocates a stamp buffer;
+        not under graph capture).  ``trace(False)`` frees it."""
+        lib = _lib.load()
+        _lib._check(lib.sc_decode_plan_trace(self._handle, 1 if enable else 0), "sc_decode_plan_trace")
+
+    def read_trace(self):
+        """Stamps of the last launch: int64 [workgroups, ops, 4] in microseconds from
+        the earliest stamp (per op: items computed, output published, input polled,
+        input staged), synchronously."""
+        import numpy as np
+        lib = _lib.load()
+        P, n = ctypes.c_int(), ctypes.c_int()
+        _lib._check(lib.sc_decode_plan_read_trace(self._handle, None, 0, ctypes.byref(P), ctypes.byref(n)),
+                    "sc_decode_plan_read_trace")
+        buf = np.zeros(P.value * n.value * 4, dtype=np.uint32)
+        _lib._check(lib.sc_decode_plan_read_trace(self._handle, ctypes.c_void_p(buf.ctypes.data), buf.size,
+                                                  ctypes.byref(P), ctypes.byref(n)), "sc_decode_plan_read_trace")
+        t = buf.reshape(P.value, n.value, 4).astype(np.int64)
+        t = t - t[t > 0].min()
+        return t.astype(np.float64) * 0.01          # 100 MHz clock -> us
+
+    def timeline(self):
+        """Per op kind, averaged over the layers away from the ends, in microseconds:
+        ``span`` (op staged to the next op staged, on the slowest workgroup),
+        ``work`` (median and max over workgroups of staged -> computed), ``straggle``
+        (slowest workgroup's publish after the median one's), ``publish`` (computed ->
+        published), ``exchange`` (slowest producer's publish -> median consumer's
+        input polled) and ``stage`` (polled -> staged) of the op that follows."""
+        import numpy as np
+        t = self.read_trace()
+        comp, pub, pol, stg = t[..., 0], t[..., 1], t[..., 2], t[..., 3]
+        nops = t.shape[1]
+        L = (nops - 1) // 6
+        mid = range(1, L - 1) if L >= 3 else range(L)     # layers away from the ends
+        out = {}
+        for k, name in enumerate(self.OP_KINDS):
+            js = [1 + 6 * l + k for l in mid if 1 + 6 * l + k + 1 < nops]
+
+            def avg(f):
+                return float(np.mean([f(j) for j in js]))
+            out[name] = {
+                "span": avg(lambda j: stg[:, j + 1].max() - stg[:, j].max()),
+                "work_median": avg(lambda j: np.median(comp[:, j] - stg[:, j])),
+                "work_max": avg(lambda j: (comp[:, j] - stg[:, j]).max()),
+                "straggle": avg(lambda j: pub[:, j].max() - np.median(pub[:, j])),
+                "publish": avg(lambda j: np.median(pub[:, j] - comp[:, j])),
+                "exchange": avg(lambda j: np.median(pol[:, j + 1]) - pub[:, j].max()),
+                "stage_next": avg(lambda j: np.median(stg[:, j + 1] - pol[:, j + 1])),
+            }
+        per_layer = float(np.mean([stg[:, 1 + 6 * (l + 1)].max() - stg[:, 1 + 6 * l].max()
+                                   for l in mid if 1 + 6 * (l + 1) < nops]))
+        return {"per_layer_us": per_layer, "ops": out}
+
     def close(self):
         h = getattr(self, "_handle", None)
         if h is not None and h.value:

@@ -263,3 +263,41 @@ def test_plan_rejects_unsupported_shapes():
     with pytest.raises(ValueError):
         TrunkPlan(m, c, torch.zeros(1, dtype=torch.int32, device="cuda"),
                   torch.zeros(1024, dtype=torch.bfloat16, device="cuda"))
+
+
+def test_trunk_op_timeline(small_w4):
+    """The plan's op timeline: with tracing on, every workgroup stamps every op in
+    order (items computed <= published, input polled <= staged, staged before the
+    op's items are computed), the outputs equal an untraced launch's, and the
+    per-op-kind summary spans the launch."""
+    m = small_w4
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(6)
+    ids = torch.randint(0, m.vocab_size, (1, 40), generator=gen, device="cuda")
+    ca = m.new_cache(1, 128)
+    logits, _ = asyncio.run(m.forward(ids, past_key_values=ca, use_cache=True, last_only=True))
+    cb = clone_cache(m, ca)
+    outs = []
+    for c, traced in ((ca, False), (cb, True)):
+        t = torch.zeros((1, 8), dtype=torch.int32, device="cuda")
+        d = DecodeGraph(m, c, t, use_graph=False, fused_trunk=True)
+        if traced:
+            d.bufs.plan.trace(True)
+        _lib.argmax(logits.reshape(1, -1), ids=d.bufs.ids.view(-1), tokens=t, step=c.counters[1:])
+        _lib.add_i32(c.counters[1:], 1, n=1)
+        d.run(2)
+        torch.cuda.synchronize()
+        assert d.bufs.plan.status() == 0
+        outs.append((t.clone(), c.k.clone(), c.vt.clone()))
+        if traced:
+            st = d.bufs.plan.read_trace()
+            P, nops, _ = st.shape
+            assert nops == 1 + 6 * len(m.layers) and P == torch.cuda.get_device_properties(0).multi_processor_count
+            comp, pub, pol, stg = st[..., 0], st[..., 1], st[..., 2], st[..., 3]
+            assert (pub >= comp).all() and (stg >= pol).all() and (comp >= stg).all()
+            assert (pol[:, 1:] >= pub[:, :-1]).all()
+            tl = d.bufs.plan.timeline()
+            assert set(tl["ops"]) == set(TrunkPlan.OP_KINDS) and tl["per_layer_us"] > 0
+            d.bufs.plan.trace(False)
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
