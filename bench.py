@@ -82,6 +82,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--kernels-only", action="store_true",
                    help="build the weights and run only the per-launch GEMV pass (for counter profiling)")
+    p.add_argument("--gemm-only", action="store_true",
+                   help="build the weights and run only the prefill quantized GEMM timing (for counter profiling)")
     p.add_argument("--trunk-only", action="store_true",
                    help="prefill, then only eager whole-trunk decode launches (for counter profiling)")
     p.add_argument("--trunk-timeline", action="store_true",
@@ -644,6 +646,12 @@ def main():
         torch.cuda.synchronize()
         ls = eager_gemv_passes(model, B, args.bits, args.kernel_reps)
         log(f"kernels-only: 3 copies of {src.numel()} bytes, {args.kernel_reps} x {len(ls)} quantized products")
+        return
+
+    if args.gemm_only:
+        gemm = time_prefill_gemms(model, P * B, args.bits, args.kernel_reps)
+        log(f"gemm-only: {args.kernel_reps} launches per shape at M = {P * B}, "
+            f"{gemm['achieved']} TFLOP/s over the four shapes")
         return
 
     gen = torch.Generator(device="cuda")
