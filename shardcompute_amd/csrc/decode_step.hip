@@ -108,14 +108,20 @@ struct Args {
     uint32_t *trace;          // null, or [P][nops][4] real-time stamps of the last launch
 };
 
+// The exchange words are accessed through global-address-space pointers: the kernel
+// reads its buffer pointers from LDS, so the compiler cannot infer the address space
+// and would emit FLAT instructions, which also count against lgkmcnt.  Every LDS or
+// scalar-load wait of the control wave would then wait for its outstanding exchange
+// stores and polls as well.  Global instructions count against vmcnt only.
+typedef __attribute__((address_space(1))) unsigned long long global_u64;
+
 __device__ __forceinline__ void ll_store(uint2 *p, uint32_t data, uint32_t ep) {
     const unsigned long long v = (unsigned long long)data | ((unsigned long long)ep << 32);
-    __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((global_u64 *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ unsigned long long ll_load(const uint2 *p) {
-    return __hip_atomic_load(reinterpret_cast<const unsigned long long *>(p), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load((const global_u64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ unsigned long long now() { return __builtin_amdgcn_s_memrealtime(); }
