@@ -64,7 +64,7 @@ constexpr int RMAX = 4;                     // query heads per kv head
 
 constexpr int NT = 6;                       // ops per layer, in this order:
 enum OpKind { K_QKV = 0, K_ATTN = 1, K_MERGE = 2, K_O = 3, K_GU = 4, K_DOWN = 5 };
-enum OpFlags { F_NORM = 1, F_SWIGLU = 2, F_RESID = 4 };
+enum OpFlags { F_NORM = 1, F_SWIGLU = 2, F_RESID = 4, F_ROW8 = 8 };
 enum Buf { B_H = 0, B_QKV, B_PART, B_ATT, B_HMID, B_ACT, B_COUNT };
 
 // Shape of one of the four projections of a layer (the same in every layer).
@@ -75,7 +75,7 @@ struct GemvDesc {
     int flags, in_buf, out_buf;
     const uint2 *in;        // LL words of the input and the output (exchange buffers in_buf, out_buf)
     uint2 *out;
-    int tb, ntl;            // this workgroup's tiles [tb, tb + ntl) (set in LDS at launch)
+    int rb, re, ntl;        // this workgroup's rows [rb, re), in ntl 16-row tiles from rb (set in LDS at launch)
 };
 
 // Device pointers of one layer: projections q|k|v, o, gate|up, down; norms; cache.
@@ -130,6 +130,27 @@ __device__ __forceinline__ unsigned long long now() { return __builtin_amdgcn_s_
 __device__ __forceinline__ void gemv_tiles(int T, int wg, int P, int &tb, int &te) {
     tb = (int)((unsigned)wg * (unsigned)T / (unsigned)P);
     te = (int)((unsigned)(wg + 1) * (unsigned)T / (unsigned)P);
+}
+
+// Rows [rb, re) of a projection owned by workgroup wg of P, covered by ntl 16-row
+// tiles from rb: contiguous ranges of whole tiles, or with F_ROW8 of 8-row halves,
+// when that evens out the rows per workgroup (q|k|v's 384 tiles on 256 CUs: 24 rows
+// each instead of 16 or 32).  A last tile with 8 rows loads its last row in place of
+// the 8 it does not own and publishes only its own rows.  SwiGLU tiles (8 gate + 8 up
+// rows) are whole tiles, with rb = 16 x the first tile.
+__device__ __forceinline__ void gemv_rows(const GemvDesc &g, int wg, int P, int &rb, int &re, int &ntl) {
+    int b, e;
+    if (g.flags & F_ROW8) {
+        gemv_tiles((g.N + 7) >> 3, wg, P, b, e);
+        rb = 8 * b;
+        re = min(8 * e, g.N);
+        ntl = (e - b + 1) >> 1;
+    } else {
+        gemv_tiles(g.T, wg, P, b, e);
+        rb = 16 * b;
+        re = min(16 * e, g.N);
+        ntl = e - b;
+    }
 }
 
 __device__ __forceinline__ int gemv_index(int kind) {
@@ -250,9 +271,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         }
         if (lane < 4) {
             GemvDesc g = lane == 0 ? a.gd[0] : lane == 1 ? a.gd[1] : lane == 2 ? a.gd[2] : a.gd[3];
-            int te;
-            gemv_tiles(g.T, wg, P, g.tb, te);
-            g.ntl = te - g.tb;
+            gemv_rows(g, wg, P, g.rb, g.re, g.ntl);
             sgd[lane] = g;
         }
         if (lane == 0) {
@@ -268,9 +287,9 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 } else if (k != K_MERGE) {
                     const int gi = gemv_index(k);
                     const GemvDesc g = gi == 0 ? a.gd[0] : gi == 1 ? a.gd[1] : gi == 2 ? a.gd[2] : a.gd[3];
-                    int tb, te;
-                    gemv_tiles(g.T, wg, P, tb, te);
-                    n = (te - tb) * g.cpt;
+                    int rb, re, nt;
+                    gemv_rows(g, wg, P, rb, re, nt);
+                    n = nt * g.cpt;
                 }
                 acc += n;
             }
@@ -534,7 +553,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                         ll_store(a.buf[B_H] + w, inr ? row[w] : 0u, ep);
                 } else {
                     const GemvDesc &o = sgd[gemv_index(kp)];
-                    const int tb = o.tb, ntl = o.ntl, cpt = o.cpt;
+                    const int ntl = o.ntl, cpt = o.cpt;
                     uint2 *dst = o.out;
                     uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
                     if (o.flags & F_SWIGLU) {
@@ -547,17 +566,18 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             chunk_sums(pp + 8 + c, cpt, u0, u1);
                             const uint32_t o0 = f2bf(silu_mul_f(bf2f(f2bf(g0)), bf2f(f2bf(u0))));
                             const uint32_t o1 = f2bf(silu_mul_f(bf2f(f2bf(g1)), bf2f(f2bf(u1))));
-                            ll_store(dst + ((tb + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
+                            ll_store(dst + (((o.rb >> 4) + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
                         }
                     } else {
                         const uint32_t *hw = reinterpret_cast<const uint32_t *>(hbuf);
                         const bool resid = o.flags & F_RESID;
                         for (int wdx = lane; wdx < ntl * 8; wdx += 64) {
                             const int tl = wdx >> 3, c = 2 * (wdx & 7);
+                            const int n = o.rb + tl * 16 + c;
+                            if (n >= o.re) continue;                    // a half tile's duplicate rows
                             const float *pp = part + (size_t)tl * cpt * 16;
                             float v0 = 0.f, v1 = 0.f;
                             chunk_sums(pp + c, cpt, v0, v1);
-                            const int n = (tb + tl) * 16 + c;
                             uint32_t o0 = f2bf(v0), o1 = f2bf(v1);
                             if (resid) {
                                 const uint32_t hv = hw[n / 2];
@@ -766,12 +786,6 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
 #pragma unroll
     for (int k = 0; k < NT; ++k) pre[k] = s_pre[k];
     const unsigned ipl_magic = ipl > 1 ? (unsigned)((0x100000000ULL + (unsigned)ipl - 1) / (unsigned)ipl) : 0u;
-    int tbk[4];                                 // first tile of this workgroup per projection
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        int te;
-        gemv_tiles(sgd[i].T, wg, P, tbk[i], te);
-    }
     struct ItemLoc {
         int l, k, i, ch;
     };
@@ -800,14 +814,15 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             const int tl = cpt == 1 ? w.i : (int)__umulhi((unsigned)w.i, o.cpt_magic);
             const int ch = w.i - tl * cpt;
             w.ch = ch;
-            const int n0 = (tbk[gi] + tl) * 16;
+            const int n0 = o.rb + tl * 16;             // this workgroup's rows [o.rb, o.re)
+            const int rlast = o.re - 1;
             const uint32_t row_bytes = (uint32_t)o.K * BITS / 8;        // every weight matrix < 4 GB
             const bool swiglu = o.flags & F_SWIGLU;
-            const int half = o.half, N = o.N;
+            const int half = o.half;
             const uint32_t G = (uint32_t)o.G;
             auto wrow = [&](int rr) -> uint32_t {
                 if (swiglu) return (uint32_t)((rr < 8 ? 0 : half - 8) + (n0 >> 1) + rr);
-                return (uint32_t)min(n0 + rr, N - 1);
+                return (uint32_t)min(n0 + rr, rlast);
             };
             const uint8_t *wq = reinterpret_cast<const uint8_t *>(lp.wq[gi]) + ch * 256;
             const uint32_t dq[4] = {dst, d1, d2, d3};
@@ -1147,6 +1162,8 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
         g.cpt = K / (m->bits == 4 ? 512 : 256);
         g.cpt_magic = g.cpt > 1 ? (unsigned)((0x100000000ULL + (unsigned long long)g.cpt - 1) / (unsigned long long)g.cpt) : 0u;
         g.half = (flags & F_SWIGLU) ? N / 2 : 0;
+        // 8-row ranges when they lower the most rows a workgroup owns (gemv_rows)
+        if (!(flags & F_SWIGLU) && ((N + 7) / 8 + P - 1) / P * 8 < (g.T + P - 1) / P * 16) flags |= F_ROW8;
         g.flags = flags; g.in_buf = in_buf; g.out_buf = out_buf;
         return g;
     };
@@ -1177,8 +1194,9 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     const int Kmax = std::max({hid, I, H * D});
     int max_items = 0;
     for (int i = 0; i < 4; ++i) {
-        const int tiles = (a.gd[i].T + P - 1) / P;
-        max_items = std::max(max_items, tiles * a.gd[i].cpt);
+        const GemvDesc &g = a.gd[i];
+        const int tiles = (g.flags & F_ROW8) ? (((g.N + 7) / 8 + P - 1) / P + 1) / 2 : (g.T + P - 1) / P;
+        max_items = std::max(max_items, tiles * g.cpt);
     }
     size_t off = (size_t)WORKERS * TRING * SLOT;
     // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 2) floats
