@@ -141,16 +141,28 @@ __device__ __forceinline__ float rms_root(float tot, int D, float eps) {
     return __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)D), eps));
 }
 
+// h / root, correctly rounded, with one division per row instead of one per element:
+// y = RN(1 / root) (the caller's), q = RN(h y), then RN(q + r y) with the remainder
+// r = h - q root, exact in one fma.  With y within half an ulp of 1 / root and q within
+// one ulp of h / root this is the correctly rounded quotient (Markstein's correction
+// step), barring overflow and underflow; root is a positive RMS and the quotients of
+// bf16 activations are normal.
+__device__ __forceinline__ float div_root(float h, float root, float y) {
+    const float q = mul_rn(h, y);
+    return fmaf(fmaf(-q, root, h), y, q);
+}
+
 // bf16((h / root) * w): divide by the root, then scale (transformer.py:55).  Every
 // kernel that normalises (standalone, the GEMV prologues, the decode trunk) uses this,
 // so they agree bit for bit; the rounding is RNE in one instruction per pair (a NaN
 // input stays NaN, its payload may differ from f2bf's)
 __device__ __forceinline__ uint4 norm_bf16x8(uint4 h, uint4 w, float root) {
+    const float y = __fdiv_rn(1.f, root);        // loop-invariant where the row's root is
     uint32_t o[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        o[e] = cvt_pk_bf16(mul_rn(__fdiv_rn(bfe(h, 2 * e), root), bfe(w, 2 * e)),
-                           mul_rn(__fdiv_rn(bfe(h, 2 * e + 1), root), bfe(w, 2 * e + 1)));
+        o[e] = cvt_pk_bf16(mul_rn(div_root(bfe(h, 2 * e), root, y), bfe(w, 2 * e)),
+                           mul_rn(div_root(bfe(h, 2 * e + 1), root, y), bfe(w, 2 * e + 1)));
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
