@@ -125,8 +125,15 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     const int nitems = my_tiles * nchunks;
 
     // ---- 1. x words for LDS (first round issued before any weight load)
-    constexpr int XR = 4;   // x words held per thread per round
+    // x words held per thread per round: the registers are free before the stream,
+    // except in the 16-wave variants (128 VGPRs)
+    constexpr int XR = MROWS <= 8 ? 4 : 16;
     const int xwords = M * Wr;
+    // word idx is (row idx / Wr, word idx % Wr): the quotient as a multiply-high by
+    // ceil(2^32 / Wr), exact for idx * Wr < 2^32 (idx < 32 x 2048, Wr <= 2048); a
+    // division by a run-time value would cost tens of instructions per word
+    const unsigned wr_magic = (unsigned)((0x100000000ULL + (unsigned)Wr - 1) / (unsigned)Wr);
+    auto xrow = [&](int idx) -> int { return Wr == 1 ? idx : (int)__umulhi((unsigned)idx, wr_magic); };
     uint4 xv[XR];
     int round_base = 0;
     auto x_issue = [&](int base) {
@@ -134,19 +141,28 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
         for (int r = 0; r < XR; ++r) {
             const int idx = base + tid + r * blockDim.x;
             if (idx < xwords) {
-                const int m = idx / Wr, w = idx - (idx / Wr) * Wr;
+                const int m = xrow(idx), w = idx - m * Wr;
                 xv[r] = *reinterpret_cast<const uint4 *>(a.x + (size_t)m * a.K + (size_t)g_begin * 64 + (size_t)w * 8);
             }
         }
     };
+    // stores a round's words and the 64-element group sums of x: the 8 words of a
+    // group are 8 adjacent lanes (Wr, the block size and every round base are
+    // multiples of 8), each lane sums its word in order, then a 3-step lane tree
     auto x_store = [&](int base) {
 #pragma unroll
         for (int r = 0; r < XR; ++r) {
             const int idx = base + tid + r * blockDim.x;
-            if (idx < xwords) {
-                const int m = idx / Wr, w = idx - (idx / Wr) * Wr;
+            const bool in = idx < xwords;
+            const int m = xrow(idx), w = idx - m * Wr;
+            float g = 0.f;
+            if (in) {
                 xl[m * xstride + w] = BITS == 4 ? permute_w4_word(xv[r]) : xv[r];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) g += bf2f(u4h(xv[r], e));
             }
+            g = group8_sum(g);                      // lanes converged: the round loop is uniform
+            if (in && (w & 7) == 0) xs[m * Gr + (w >> 3)] = g;
         }
     };
     x_issue(0);
@@ -182,18 +198,6 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     for (round_base = XR * blockDim.x; round_base < xwords; round_base += XR * blockDim.x) {
         x_issue(round_base);
         x_store(round_base);
-    }
-    __syncthreads();
-    for (int idx = tid; idx < M * Gr; idx += blockDim.x) {
-        const int m = idx / Gr, gl = idx - (idx / Gr) * Gr;
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const uint4 v = xl[m * xstride + gl * 8 + w];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) sum += bf2f(u4h(v, e));
-        }
-        xs[m * Gr + gl] = sum;
     }
     __syncthreads();
 
