@@ -17,7 +17,7 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
                      const DmaFused *fused = nullptr);
 bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K);
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc);
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half = 0);
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -241,6 +241,11 @@ static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw,
         if (rc) return rc;
     }
     if (!swiglu_half) return qmm_dispatch(xin, wq, s, b, bias, y, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
+    if (M > 8 && M <= 32) {
+        // the 9-32-row GEMV's split-K pass applies silu(gate) * up itself
+        rc = launch_qgemv16(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
     rc = qmm_dispatch(xin, wq, s, b, bias, gu_scratch, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
     if (rc) return rc;
     return launch_silu_mul(gu_scratch, M, swiglu_half, y, st);

@@ -43,7 +43,7 @@ struct Gemv16Args {
     const uint16_t *b;
     const uint16_t *bias;
     uint16_t *y;
-    float *partials;       // [splits, M, N] when gridDim.y > 1
+    float *partials;       // [splits, M, N] fp32 partials (null: the kernel writes y itself)
     int M, N, K, G;
     int spans_per_split;   // multiple of CHUNK_SPANS
     int tiles_per_wg;      // 16-column tiles of one workgroup (its waves take them in turn)
@@ -296,7 +296,7 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
                     const int m = (BITS == 4 && MROWS <= 8) ? 4 * q + r : 16 * h + 4 * q + r;
                     if (m < M) {
                         const float v = fin[h][r];
-                        if (gridDim.y == 1) {
+                        if (!a.partials) {
                             uint32_t o = f2bf(v);
                             if (a.bias) o = f2bf(bf2f(o) + bf2f(a.bias[nn]));
                             a.y[(size_t)m * N + nn] = (uint16_t)o;
@@ -324,15 +324,28 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
 }
 
 // Sums split partials in split order, rounds to bf16, adds the bias after rounding.
+// With half > 0 the product is gate|up stacked (N = 2 half) and y [M, half] receives
+// bf16(silu(gate) * up) of the rounded values, as silu_mul_kernel computes it from
+// the bf16 product (parallel/mlp.py:161-162, 241-245).
 __global__ void __launch_bounds__(256) qgemv_finalize_kernel(const float *partials, int splits, int M, int N,
-                                                              const uint16_t *bias, uint16_t *y) {
+                                                              const uint16_t *bias, uint16_t *y, int half) {
     const int64_t total = (int64_t)M * N;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    auto value = [&](int64_t i) -> uint32_t {          // rounded product element i (+ bias)
         float v = 0.f;
         for (int s = 0; s < splits; ++s) v += partials[(size_t)s * total + i];
         uint32_t o = f2bf(v);
         if (bias) o = f2bf(bf2f(o) + bf2f(bias[i % N]));
-        y[i] = (uint16_t)o;
+        return o;
+    };
+    const int64_t nout = half ? (int64_t)M * half : total;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nout; i += (int64_t)gridDim.x * blockDim.x) {
+        if (!half) {
+            y[i] = (uint16_t)value(i);
+        } else {
+            const int64_t m = i / half, c = i - m * half;
+            const uint32_t g = value(m * N + c), u = value(m * N + half + c);
+            y[i] = (uint16_t)f2bf(silu_mul_f(bf2f(g), bf2f(u)));
+        }
     }
 }
 
@@ -423,9 +436,12 @@ static int launch_gemv16_t(const Gemv16Args &a, const Gemv16Plan &p, hipStream_t
 // Returns SC_EUNSUPPORTED when the shape does not suit this kernel (caller falls back).
 // no_alloc: the split-K partials go to the file-scope scratch array (shapes that
 // need more than it holds are rejected) instead of the library-owned buffer.
+// swiglu_half > 0: the weight is gate|up stacked (N = 2 swiglu_half) and y [M, swiglu_half]
+// receives silu(gate) * up, applied by the partials' pass (which then always runs).
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc) {
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half) {
     if (M < 1 || M > 32) return SC_EUNSUPPORTED;
+    if (swiglu_half && (swiglu_half < 0 || N != 2 * swiglu_half)) return SC_EUNSUPPORTED;
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16)) return SC_EUNSUPPORTED;
     Gemv16Plan p;
     const bool ok = bits == 4 ? plan_gemv16<4>(M, N, K, &p) : plan_gemv16<8>(M, N, K, &p);
@@ -434,7 +450,8 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y; a.partials = nullptr;
     a.M = M; a.N = N; a.K = K; a.G = K / 64; a.spans_per_split = p.spans_per_split;
     a.tiles_per_wg = p.tiles_per_wg;
-    if (p.splits > 1) {
+    const bool with_partials = p.splits > 1 || swiglu_half > 0;
+    if (with_partials) {
         const size_t need = (size_t)p.splits * M * N;
         if (no_alloc) {
             constexpr size_t cap = SC_QMM_NOALLOC_SCRATCH_BYTES / sizeof(float);
@@ -458,12 +475,12 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     return set_error(SC_EUNSUPPORTED, "qgemv16: bits=%d", bits);
 #undef SC_G16
     if (rc) return rc;
-    if (p.splits > 1) {
-        const int64_t total = (int64_t)M * N;
+    if (with_partials) {
+        const int64_t total = (int64_t)M * (swiglu_half ? swiglu_half : N);
         int64_t blocks = (total + 255) / 256;
         if (blocks > 4096) blocks = 4096;
         hipLaunchKernelGGL(qgemv_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.partials, p.splits,
-                           M, N, bias, y);
+                           M, N, bias, y, swiglu_half);
         SC_HIP_CHECK(hipGetLastError());
     }
     return SC_OK;

@@ -64,7 +64,8 @@ def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
 @pytest.mark.parametrize("M,I,K,bits,norm", [(1, 14336, 4096, 4, True), (1, 5632, 2048, 4, False),
                                               (3, 1024, 1024, 8, True), (12, 512, 1024, 4, True),
                                               (1, 2048, 576, 4, True), (1, 256, 512, 4, True),
-                                              (1, 64, 512, 8, False)])
+                                              (1, 64, 512, 8, False), (16, 1792, 4096, 4, True),
+                                              (32, 896, 2048, 8, False), (24, 1024, 3584, 4, False)])
 def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     rng = np.random.default_rng(M * 7 + I + K)
     wq, s, b = _weights(rng, 2 * I, K, bits)
@@ -89,12 +90,33 @@ def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     # moves by a bf16 step of g or u (measured relative to the output's scale)
     a1, a2 = host_u16(act), host_u16(act2)
     assert max_abs_rel(a1, a2) <= 2e-3 and (bf16_ulp_diff(a1, a2) > 0).mean() < 0.02
+    if 8 < M <= 32:
+        # 9-32 rows: the product's own split-K pass applies the gate, on the same sums
+        assert torch.equal(act, act2)
     xin = host_u16(xn2)
     gu = quantized_matmul_f64(xin, wq, s, b, 64, bits)
     g = bf16_to_f32(f32_to_bf16(gu[:, :I].astype(np.float32)))
     u = bf16_to_f32(f32_to_bf16(gu[:, I:].astype(np.float32)))
     ref = bf16_to_f32(f32_to_bf16((g / (np.float32(1) + np.exp(-g, dtype=np.float32))) * u))
     assert max_abs_rel(host_u16(act), ref) <= LINEAR_TOL
+
+
+@pytest.mark.parametrize("M,bits", [(9, 4), (16, 8), (32, 4)])
+def test_qmm_swiglu_batch_with_bias(device, M, bits):
+    """9-32 rows: silu(gate) * up from the GEMV's split-K pass, with a linear bias
+    added to the rounded gate and up (as the plain product does), equals the plain
+    product followed by silu_mul bit for bit."""
+    rng = np.random.default_rng(M + 1000 * bits)
+    I, K = 1536, 4096
+    wq, s, b = _weights(rng, 2 * I, K, bits)
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd = dev_bf16(_bf(rng, (M, K)))
+    bias = dev_bf16(_bf(rng, (2 * I,), 0.1))
+    print(f"qmm_swiglu bias M={M} W{bits}", flush=True)
+    act, _ = _lib.qmm_swiglu(xd, *W, bias=bias, bits=bits)
+    act2 = _lib.silu_mul(_lib.qmm(xd, *W, bias=bias, bits=bits))
+    torch.cuda.synchronize()
+    assert torch.equal(act, act2)
 
 
 def test_gemv_is_reproducible(device):
