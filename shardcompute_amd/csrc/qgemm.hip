@@ -33,6 +33,7 @@ struct GemmArgs {
     const uint16_t *bias;
     uint16_t *y;
     int M, N, K, G;
+    int ldy;               // y's row stride (N, or wider when this launch covers a column range)
     int mt, nt, tiles;     // m-tiles, n-tiles, real tiles (the grid is padded to a multiple of 8)
 };
 
@@ -268,7 +269,7 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
             const int n = n0 + wn * Gm::WN + j * 32 + li;
             if (n >= N) continue;
             const float bb = a.bias ? bf2f(a.bias[n]) : 0.f;
-            uint16_t *yc = a.y + (size_t)mw * N + n;
+            uint16_t *yc = a.y + (size_t)mw * a.ldy + n;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
 #pragma unroll
@@ -276,14 +277,66 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
                     uint32_t o = cvt_pk_bf16(acc[i][j][r], acc[i][j][r + 1]);
                     if (a.bias) o = cvt_pk_bf16(bf2f(o & 0xFFFFu) + bb, bf2f(o >> 16) + bb);
                     const int dm = i * 32 + 8 * (r >> 2) + (r & 3);
-                    if (!CHK || mw + dm < M) yc[(size_t)dm * N] = (uint16_t)o;
-                    if (!CHK || mw + dm + 1 < M) yc[(size_t)(dm + 1) * N] = (uint16_t)(o >> 16);
+                    if (!CHK || mw + dm < M) yc[(size_t)dm * a.ldy] = (uint16_t)o;
+                    if (!CHK || mw + dm + 1 < M) yc[(size_t)(dm + 1) * a.ldy] = (uint16_t)(o >> 16);
                 }
             }
         }
     };
     if (m0 + BM <= M) store_tile(std::false_type{});
     else store_tile(std::true_type{});
+}
+
+// One launch over the product's columns [n0, n0 + Nc) with BN-wide tiles.
+template <int BITS, int BN>
+static int launch_qgemm_cols(const GemmArgs &full, int n0, int Nc, hipStream_t stream) {
+    GemmArgs a = full;
+    a.wq = full.wq + (size_t)n0 * ((size_t)full.K * BITS / 32);
+    a.s = full.s + (size_t)n0 * full.G;
+    a.b = full.b + (size_t)n0 * full.G;
+    a.bias = full.bias ? full.bias + n0 : nullptr;
+    a.y = full.y + n0;
+    a.N = Nc;
+    a.nt = (Nc + BN - 1) / BN;
+    a.tiles = a.mt * a.nt;
+    const long blocks = ((long)a.tiles + XCDS - 1) / XCDS * XCDS;
+    if (blocks > 0x7FFFFFFFL) return set_error(SC_EINVAL, "qgemm: grid too large");
+    if (device_info().max_lds_per_block < Geo<BN>::LDS) return set_error(SC_EUNSUPPORTED, "qgemm: LDS too small");
+    auto kern = qgemm_mfma_kernel<BITS, BN>;
+    static bool configured = false;
+    if (!configured) {
+        SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, Geo<BN>::LDS));
+        configured = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(THREADS), Geo<BN>::LDS, stream, a);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+template <int BITS>
+static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream) {
+    // The tile width with the shorter estimated time: waves of tiles over the CUs times
+    // the cost of one tile, a 128-wide tile costing 0.64 of a 256-wide one (measured
+    // on the Llama-3-8B shapes at M = 2048: it reads more LDS per MFMA).  One partial
+    // wave of wide tiles beats two waves of narrow ones.
+    const int cus = device_info().num_cus;
+    const int N = a.N, mt = a.mt;
+    const long tiles256 = (long)mt * ((N + 255) / 256);
+    const long waves256 = (tiles256 + cus - 1) / cus;
+    const long waves128 = ((long)mt * ((N + 127) / 128) + cus - 1) / cus;
+    if (!(100 * waves256 <= 64 * waves128)) return launch_qgemm_cols<BITS, 128>(a, 0, N, stream);
+    // Wide tiles leaving a partial last round (gate|up at M = 2048: 896 tiles on 256
+    // CUs, 3.5 rounds of work in 4): the columns of that round go to a second launch
+    // of 128-wide tiles, which fill one round at ~0.64 of a wide tile's time.
+    const long r = tiles256 % cus;
+    if (r > 0 && tiles256 > cus && N % 256 == 0 && r % mt == 0 && 2 * r <= cus) {
+        const int n1 = N - (int)(r / mt) * 256;
+        const int rc = launch_qgemm_cols<BITS, 256>(a, 0, n1, stream);
+        if (rc) return rc;
+        return launch_qgemm_cols<BITS, 128>(a, n1, N - n1, stream);
+    }
+    return launch_qgemm_cols<BITS, 256>(a, 0, N, stream);
 }
 
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -293,39 +346,13 @@ int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
     if (K % BK) return set_error(SC_EINVAL, "qgemm: K=%d not a multiple of %d", K, BK);
     if (((uintptr_t)x % 16) || ((uintptr_t)wq % 16))
         return set_error(SC_EINVAL, "qgemm: x and wq must be 16-byte aligned");
-    // The tile width with the shorter estimated time: waves of tiles over the CUs times
-    // the cost of one tile, a 128-wide tile costing 0.64 of a 256-wide one (measured
-    // on the Llama-3-8B shapes at M = 2048: it reads more LDS per MFMA).  One partial
-    // wave of wide tiles beats two waves of narrow ones.
-    const int cus = device_info().num_cus;
-    const int mt = (M + BM - 1) / BM;
-    const long waves256 = ((long)mt * ((N + 255) / 256) + cus - 1) / cus;
-    const long waves128 = ((long)mt * ((N + 127) / 128) + cus - 1) / cus;
-    const bool wide = 100 * waves256 <= 64 * waves128;
-    const int BNv = wide ? 256 : 128;
-    const int lds = wide ? Geo<256>::LDS : Geo<128>::LDS;
-    if (device_info().max_lds_per_block < lds) return set_error(SC_EUNSUPPORTED, "qgemm: LDS too small");
     GemmArgs a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
     a.M = M; a.N = N; a.K = K; a.G = K / BK;
-    a.mt = mt;
-    a.nt = (N + BNv - 1) / BNv;
-    a.tiles = a.mt * a.nt;
-    const long blocks = ((long)a.tiles + XCDS - 1) / XCDS * XCDS;
-    if (blocks > 0x7FFFFFFFL) return set_error(SC_EINVAL, "qgemm: grid too large");
-    static bool cfg[2][2] = {};
-    auto go = [&](auto kern, bool &c) -> int {
-        if (!c) {
-            SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds));
-            c = true;
-        }
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(THREADS), lds, stream, a);
-        SC_HIP_CHECK(hipGetLastError());
-        return SC_OK;
-    };
-    if (bits == 4) return wide ? go(qgemm_mfma_kernel<4, 256>, cfg[0][0]) : go(qgemm_mfma_kernel<4, 128>, cfg[0][1]);
-    return wide ? go(qgemm_mfma_kernel<8, 256>, cfg[1][0]) : go(qgemm_mfma_kernel<8, 128>, cfg[1][1]);
+    a.ldy = N;
+    a.mt = (M + BM - 1) / BM;
+    a.nt = a.tiles = 0;
+    return bits == 4 ? launch_qgemm_t<4>(a, stream) : launch_qgemm_t<8>(a, stream);
 }
 
 }  // namespace sc

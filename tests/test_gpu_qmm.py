@@ -152,6 +152,27 @@ def test_full_size_prefill_shapes(device, bits, K, N):
         assert max_abs_rel(y, host_u16(yg)) <= LINEAR_TOL
 
 
+@pytest.mark.parametrize("M,K,N,bits,with_bias", [(256, 64, 153600, 4, True), (256, 64, 153600, 8, True),
+                                                     (2048, 4096, 28672, 4, False)])
+def test_prefill_split_launch(device, M, K, N, bits, with_bias):
+    """Wide tiles that leave a partial last round over the CUs run as two launches
+    (the last round's columns with 128-wide tiles): every output, across the column
+    split and with the bias on both sides of it, against the GEMV on 32-row blocks,
+    and sampled rows against the fp64 oracle."""
+    rng = np.random.default_rng(M + K + N + bits)
+    x, wq, s, b, bias = _case(rng, M, K, N, bits, with_bias)
+    print(f"gemm split M={M} K={K} N={N} bits={bits} bias={with_bias}", flush=True)
+    y = _run(x, wq, s, b, bias, bits, _lib.PATH_GEMM)
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd, bd = dev_bf16(x), None if bias is None else dev_bf16(bias)
+    yg = torch.cat([_lib.qmm(xd[r0:r0 + 32], *W, bd, bits=bits, path=_lib.PATH_GEMV) for r0 in range(0, M, 32)])
+    assert max_abs_rel(y, host_u16(yg)) <= LINEAR_TOL
+    rows = np.sort(rng.choice(M, 8, replace=False))
+    ref = f32_to_bf16((quantized_matmul_f64(x[rows], wq, s, b, 64, bits)
+                       + (0 if bias is None else bf16_to_f32(bias).astype(np.float64))).astype(np.float32))
+    assert max_abs_rel(y[rows], ref) <= LINEAR_TOL
+
+
 def test_linearity_in_x(device):
     rng = np.random.default_rng(9)
     x1, wq, s, b, _ = _case(rng, 8, 4096, 512, 4, False)
