@@ -184,8 +184,10 @@ int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
  * xn = RMSNorm(x + residual) when norm_weight_or_null is given (xn_out and, with a
  * residual, h_out receive xn and x + residual as for sc_qmm_rmsnorm_bf16).  The
  * decode GEMV (M <= 8) pairs gate row i with up row I + i inside one tile and writes
- * act [M, I] directly; otherwise the product goes to gate_up_scratch [M, 2I] and
- * the standalone sc_silu_mul_bf16 follows.  Outputs must not overlap the inputs.
+ * act [M, I] directly; at 9-32 rows the split-K finalize rounds gate and up to bf16
+ * (bias after rounding) and writes act [M, I]; otherwise the product goes to
+ * gate_up_scratch [M, 2I] and the standalone sc_silu_mul_bf16 follows (the same
+ * values).  Outputs must not overlap the inputs.
  * Replaces ParallelMLP.forward's gate/up projections and activation
  * (src/shardcompute/parallel/mlp.py:241-245), after the post-attention layernorm
  * (transformer.py:249-250).
