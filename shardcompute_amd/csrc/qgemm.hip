@@ -239,20 +239,31 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
     for (int qt = 0; qt < 4; ++qt) store_w(w0, 0, qt);
     store_x(0);
     load_w(min(2, gl), w0);
+    // With 128-wide tiles the x rows of stage g+1 are loaded before the barrier that
+    // starts stage g (XEARLY): when all waves issue their x loads at a stage's start,
+    // the issue waits for room in the memory pipeline (about a fifth of a stage,
+    // measured), and this way it overlaps the barrier and the rows have a whole stage
+    // to arrive.  Measured at M = 2048 (medians of 8 interleaved runs): o and down
+    // 2-14 % faster; with 256-wide tiles it was 0-4 % slower, so those keep loading x
+    // at the start of the stage that stores it.
+    constexpr bool XEARLY = BN == 128;
+    if (XEARLY) load_x(min(1, gl));
     __syncthreads();
     // stage g uses buffer g & 1; w1 holds stage g+1 when g is even, w0 when odd
     for (int g = 0; g < G; g += 2) {
         // even stage g: dequant w1 (stage g+1), then load stage g+3 into w1
-        load_x(min(g + 1, gl));
+        if (!XEARLY) load_x(min(g + 1, gl));
         stage(0, w1);
         load_w(min(g + 3, gl), w1);
         store_x(1);
+        if (XEARLY) load_x(min(g + 2, gl));
         __syncthreads();
         if (g + 1 < G) {   // odd stage g+1: dequant w0 (stage g+2), then load stage g+4 into w0
-            load_x(min(g + 2, gl));
+            if (!XEARLY) load_x(min(g + 2, gl));
             stage(1, w0);
             load_w(min(g + 4, gl), w0);
             store_x(0);
+            if (XEARLY) load_x(min(g + 3, gl));
             __syncthreads();
         }
     }
