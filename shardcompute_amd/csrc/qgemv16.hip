@@ -114,8 +114,12 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     const int g_begin = sp_begin * C::SPAN_GROUPS;
     const int xstride = Wr + 1;
 
+    // x rows 0..M-1, then row M of zeros: the A operand of a lane that carries no x
+    // (a row beyond M, or the other group parity) is read from it, so every x read is
+    // unconditional (a conditional read became a branch around each LDS load, which
+    // then completed one at a time)
     uint4 *xl = reinterpret_cast<uint4 *>(smem);
-    float *xs = reinterpret_cast<float *>(smem + (size_t)M * xstride * 16);
+    float *xs = reinterpret_cast<float *>(smem + (size_t)(M + 1) * xstride * 16);
 
     // this wave's items: (tile, chunk) for its tiles wave, wave + nwaves, ... of the
     // workgroup, every chunk of the split in order
@@ -194,6 +198,7 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
     if (nitems > 0) w_issue(0, wA, sA, bA);
 
     // ---- 3. stage x (remaining rounds wait for everything; only large M*K needs them)
+    for (int w = tid; w < xstride; w += blockDim.x) xl[M * xstride + w] = make_uint4(0u, 0u, 0u, 0u);
     x_store(0);
     for (round_base = XR * blockDim.x; round_base < xwords; round_base += XR * blockDim.x) {
         x_issue(round_base);
@@ -206,15 +211,15 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
 #pragma unroll
     for (int s = 0; s < C::NSETS; ++s) acc[s] = f32x4v{0.f, 0.f, 0.f, 0.f};
 
-    // A-operand row of this lane per set, and whether it carries x for this lane-group
+    // A-operand row of this lane per set: its x row, or the zero row when it carries
+    // no x for this lane-group
     int arow[C::NSETS];
-    bool aact[C::NSETS];
 #pragma unroll
     for (int s = 0; s < C::NSETS; ++s) {
         const int v = 16 * s + j;
         const int m = C::mrow(v);
-        arow[s] = min(m, M - 1);
-        aact[s] = (m < M) && (BITS == 8 || C::parity(v) == (q >> 1));
+        const bool act = (m < M) && (BITS == 8 || C::parity(v) == (q >> 1));
+        arow[s] = act ? m : M;                          // M: the zero row
     }
     // output rows of this lane per set (D row v = 16s + 4q + r)
     int erow[C::NSETS][4];
@@ -226,17 +231,44 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
         for (int r = 0; r < 4; ++r) erow[s][r] = min(C::mrow(16 * s + 4 * q + r), M - 1);
     }
 
+    // x operands of a span: every read of the span is issued before its MFMAs, and
+    // where registers allow (at most 8 reads a span) the next span's before the
+    // current span's MFMAs, so the LDS latency is paid about once per span rather
+    // than once per MFMA (the compiler otherwise waited for each read in turn)
+    constexpr int XRD = C::NSETS * C::MFMA_PER_SET;          // x reads per span
+    constexpr bool XDB = XRD <= 8;                           // next span's reads ahead
+    auto x_read = [&](int spl, uint4 (&xa)[XRD]) {
+#pragma unroll
+        for (int s = 0; s < C::NSETS; ++s)
+#pragma unroll
+            for (int u = 0; u < C::MFMA_PER_SET; ++u) {
+                const int word = spl * C::SPAN_WORDS + (BITS == 4 ? 4 * q + u : 2 * q + u);
+                xa[s * C::MFMA_PER_SET + u] = xl[arow[s] * xstride + word];
+            }
+    };
+    // W4 dequant constants in registers the compiler cannot see through: with the
+    // literals, (w & mask) | magic became two instructions instead of one v_and_or_b32
+    uint32_t nmask = 0x000F000Fu, nmagic = 0x43004300u;
+    asm volatile("" : "+s"(nmask));
+    asm volatile("" : "+v"(nmagic));
     auto compute_chunk = [&](int cc, const uint4 *w, uint4 sv, uint4 bv) {
+        uint4 xa[2][XRD];
+        x_read(cc * CHUNK_SPANS, xa[0]);
 #pragma unroll
         for (int t = 0; t < CHUNK_SPANS; ++t) {
             const int spl = cc * CHUNK_SPANS + t;     // span index within the split
+            const int xb = XDB ? (t & 1) : 0;
+            if (XDB && t + 1 < CHUNK_SPANS) x_read(spl + 1, xa[xb ^ 1]);
+            if (!XDB && t > 0) x_read(spl, xa[0]);
             const uint4 wv = w[t];
             bf16x8_t B[C::MFMA_PER_SET];
             if (BITS == 4) {
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
                     const uint32_t ww = u4c(wv, u);
-                    B[u] = as_bf16x8(nib_pair(ww, 0), nib_pair(ww, 4), nib_pair(ww, 8), nib_pair(ww, 12));
+                    // nib_pair(ww, 0 / 4 / 8 / 12)
+                    B[u] = as_bf16x8((ww & nmask) | nmagic, ((ww >> 4) & nmask) | nmagic,
+                                     ((ww >> 8) & nmask) | nmagic, ((ww >> 12) & nmask) | nmagic);
                 }
             } else {
 #pragma unroll
@@ -250,11 +282,8 @@ __global__ void __launch_bounds__(64 * gemv16_max_waves(MROWS)) qgemv16_kernel(G
             for (int s = 0; s < C::NSETS; ++s) {
                 P[s] = f32x4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int u = 0; u < C::MFMA_PER_SET; ++u) {
-                    const int word = spl * C::SPAN_WORDS + (BITS == 4 ? 4 * q + u : 2 * q + u);
-                    const uint4 xa = aact[s] ? xl[arow[s] * xstride + word] : make_uint4(0u, 0u, 0u, 0u);
-                    P[s] = mfma16x16x32(as_bf16x8(xa), B[u], P[s]);
-                }
+                for (int u = 0; u < C::MFMA_PER_SET; ++u)
+                    P[s] = mfma16x16x32(as_bf16x8(xa[xb][s * C::MFMA_PER_SET + u]), B[u], P[s]);
             }
 #pragma unroll
             for (int s = 0; s < C::NSETS; ++s) {
@@ -403,7 +432,7 @@ static bool plan_gemv16(int M, int N, int K, Gemv16Plan *p) {
         const int cps = (nchunks + s - 1) / s;
         const int real = (nchunks + cps - 1) / cps;
         const int kr = cps * chunk_k;
-        const int lds = M * (kr / 8 + 1) * 16 + M * (kr / 64) * 4;
+        const int lds = (M + 1) * (kr / 8 + 1) * 16 + M * (kr / 64) * 4;
         if (lds <= lds_cap) {
             const int groups0 = (di.num_cus + real - 1) / real;
             const int tpw = (tiles + groups0 - 1) / groups0;
