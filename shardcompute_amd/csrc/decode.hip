@@ -779,8 +779,11 @@ void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPl
     const long base = B * Hkv * a.hgroups * a.npb;
     // split the keys into ranges when the (batch, head, position) workgroups alone
     // cannot fill the GPU; a range covers one block per wave at least, and at most
-    // 64 ranges are merged (one per lane of the combine)
-    const long target = 2L * device_info().num_cus;
+    // 64 ranges are merged (one per lane of the combine).  The attention kernels take
+    // all 256 VGPRs, so one 4-wave workgroup runs per CU: the target is one round of
+    // workgroups (two rounds of half-length ranges measured 20-28 % slower at batch
+    // 4-32 decode)
+    const long target = device_info().num_cus;
     int nsplit = 1;
     if (base < target && T_cap > ATTN_STRIDE) {
         long want = (target + base - 1) / base;
