@@ -19,7 +19,7 @@ BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libshardcompute_hip.so")
 ARCH = os.environ.get("SC_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["abi.hip", "qgemv_dma.hip", "qgemv_m1.hip", "qgemv16.hip", "qgemv.hip", "qgemm.hip", "gather.hip", "quant.hip", "decode.hip", "decode_step.hip"]
+SOURCES = ["abi.hip", "qgemv_dma.hip", "qgemv_m1.hip", "qgemv16.hip", "qgemv.hip", "qgemm.hip", "gather.hip", "quant.hip", "decode.hip", "attn_prefill.hip", "decode_step.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -33,6 +33,13 @@ HIPCC_FLAGS = [
     "-I", os.path.join(ROOT, "include"),
 ]
 
+# per-source additions: the prefill attention kernel keeps its MFMA accumulators in
+# VGPRs (it rescales them in place every few blocks; in AGPRs each block would copy
+# them to VGPRs and back)
+EXTRA_FLAGS = {
+    "attn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 
 def hipcc():
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -43,7 +50,7 @@ def hipcc():
 
 def _compile(src):
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

@@ -179,10 +179,12 @@ __device__ __forceinline__ void attn_load(AttnBlock<D> &blk, const uint16_t *kba
     }
 }
 
-// S^T, masked online softmax and O^T update for one block of 32 keys.
+// S^T, masked online softmax and O^T update for one block of 32 keys.  Cache slots
+// at or past vend may hold anything, NaN included: in the block that reaches them
+// their V pieces are zeroed, so that their zero probabilities meet no NaN.
 template <int D>
-__device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8_t *qv, int kb, int limit, int g,
-                                           float scale_log2, float &m, float &lsum, f4 *o) {
+__device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8_t *qv, int kb, int limit, int vend,
+                                           int g, float scale_log2, float &m, float &lsum, f4 *o) {
     f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < D / 32; ++u) {
@@ -212,13 +214,23 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
     m = mn;
     const bf16x8_t pb8 = as_bf16x8(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                    pack_bf16x2(p[6], p[7]));
+    // keys kb + 4g + 0..3 (piece 0) and kb + 16 + 4g + 0..3 (piece 1)
+    uint32_t mk[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
+    if (kb + ATTN_KB > vend) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = kb + 16 * (i >> 1) + 4 * g + 2 * (i & 1);
+            mk[i] = (k < vend ? 0xFFFFu : 0u) | (k + 1 < vend ? 0xFFFF0000u : 0u);
+        }
+    }
 #pragma unroll
     for (int n = 0; n < D / 16; ++n) {
         f4 acc = o[n];
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] *= alpha;
         o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            as_bf16x8(blk.v[n][0].x, blk.v[n][0].y, blk.v[n][1].x, blk.v[n][1].y), pb8, acc, 0, 0, 0);
+            as_bf16x8(blk.v[n][0].x & mk[0], blk.v[n][0].y & mk[1], blk.v[n][1].x & mk[2], blk.v[n][1].y & mk[3]),
+            pb8, acc, 0, 0, 0);
     }
 }
 
@@ -285,11 +297,11 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
     while (true) {
         const int kn = kb + ATTN_STRIDE;
         attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
-        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T, g, a.scale_log2, m, lsum, o);
         if (kn >= k_hi) break;
         const int kn2 = kn + ATTN_STRIDE;
         attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
-        attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
+        attn_block<D>(nxt, qv, kn, limit, T, g, a.scale_log2, m, lsum, o);
         if (kn2 >= k_hi) break;
         kb = kn2;
     }
@@ -540,17 +552,17 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
     // cached keys.  One block per wave (the usual decode split) needs no prefetch: a
     // useless one would also hold vmcnt slots that the append's stores then wait for.
     if (kb + ATTN_STRIDE >= k_hi) {
-        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o);
     } else {
         // the loop of attn_kernel (unconditional, clamped loads)
         while (true) {
             const int kn = kb + ATTN_STRIDE;
             attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
-            if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, g, a.scale_log2, m, lsum, o);
+            if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o);
             if (kn >= k_hi) break;
             const int kn2 = kn + ATTN_STRIDE;
             attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
-            attn_block<D>(nxt, qv, kn, limit, g, a.scale_log2, m, lsum, o);
+            attn_block<D>(nxt, qv, kn, limit, T - 1, g, a.scale_log2, m, lsum, o);
             if (kn2 >= k_hi) break;
             kb = kn2;
         }
@@ -904,6 +916,11 @@ int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H
     return SC_OK;
 }
 
+// attn_prefill.hip
+int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
+                        const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
+                        long D, float scale, hipStream_t stream);
+
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
                      long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream) {
@@ -916,6 +933,11 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
         return set_error(SC_EINVAL, "attention: bad row strides");
     if (((uintptr_t)q | (uintptr_t)kc) % 16 || ((uintptr_t)vt | (uintptr_t)out) % 8)
         return set_error(SC_EINVAL, "attention: misaligned pointers");
+    // many positions: attn_prefill_kernel (attn_prefill.hip, 128 columns a workgroup)
+    // when the shape suits it; otherwise attn_kernel, which can also split the keys
+    const int pf = launch_attn_prefill(q, q_stride, kc, vt, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
+                                       scale, stream);
+    if (pf <= 0) return pf;
     AttnPlan pl;
     plan_attention(B, S, H, Hkv, D, T_cap, &pl);
     AttnArgs a = pl.a;

@@ -113,12 +113,15 @@ def test_rope_append(device, B, S, H, Hkv, D, past, offset):
     assert not kh[:, :, mask].any() and not vh[:, :, :, mask].any()
 
 
-def _attn_case(rng, B, S, H, Hkv, D, past, extra_cap=0):
+def _attn_case(rng, B, S, H, Hkv, D, past, extra_cap=0, nan_past=False):
     T = past + S
     T_cap = ((T + extra_cap + 31) // 32) * 32
     q = _bf(rng, (B * S, H * D))
     k = _bf(rng, (B, Hkv, T_cap, D))          # finite garbage past T must be masked out
     v = _bf(rng, (B, Hkv, T_cap, D))
+    if nan_past:                              # slots past T may hold anything, NaN included
+        k[:, :, T:] = 0x7FC0
+        v[:, :, T:] = 0x7FC0
     kc = dev_bf16(k)
     vt = dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2)))
     cnt = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
@@ -146,12 +149,32 @@ def _attn_case(rng, B, S, H, Hkv, D, past, extra_cap=0):
     (2, 77, 8, 2, 64, 0, 5),          # ragged prefill, batch 2
     (1, 48, 32, 8, 128, 200, 0),      # chunked prefill after a cache
     (1, 5, 12, 4, 64, 3, 0),          # 3 heads per KV head (16 columns not filled)
+    # long prefills (128-column workgroups)
+    (1, 512, 32, 8, 128, 0, 0),       # Llama-3-8B heads
+    (1, 512, 32, 8, 128, 700, 64),    # after a cache, the length off the block grid
+    (1, 640, 32, 32, 128, 0, 0),      # no GQA: 128 positions of one head a workgroup
+    (2, 300, 64, 8, 128, 17, 0),      # 70B heads (8 per KV head), ragged, batch 2
+    (8, 130, 16, 2, 128, 0, 100),     # 8 heads per KV head, batch 8, a last block of 2 positions
 ])
 def test_attention(device, B, S, H, Hkv, D, past, extra):
     rng = np.random.default_rng(B * 7 + S * 13 + H + past)
     err = _attn_case(rng, B, S, H, Hkv, D, past, extra)
     print(f"attention B={B} S={S} H={H} Hkv={Hkv} D={D} past={past}: max-abs-rel {err:.2e}", flush=True)
     assert err <= ATTN_TOL
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,D,past,extra", [
+    (1, 48, 32, 8, 128, 200, 40),     # 16-column workgroups
+    (1, 300, 32, 8, 64, 17, 40),      # head_dim 64
+    (1, 512, 32, 8, 128, 0, 40),      # 128-column workgroups
+    (1, 640, 32, 8, 128, 250, 70),    # 128-column workgroups, the length inside a block
+])
+def test_attention_nan_past_length(device, B, S, H, Hkv, D, past, extra):
+    # cache slots at or past the length hold NaN: they must not reach the output
+    rng = np.random.default_rng(S + past)
+    err = _attn_case(rng, B, S, H, Hkv, D, past, extra, nan_past=True)
+    print(f"attention (NaN past T) B={B} S={S} H={H} Hkv={Hkv} D={D} past={past}: max-abs-rel {err:.2e}", flush=True)
+    assert np.isfinite(err) and err <= ATTN_TOL
 
 
 def _decode_case(rng, B, H, Hkv, D, past, T_cap, offset=0, base=500000.0):
