@@ -73,8 +73,11 @@ __device__ __forceinline__ uint32_t fa_kswz(int r, int c) {
     return (uint32_t)(r * 256 + ((c ^ (fa_swap23(r) & 15)) << 4));
 }
 // byte offset of 16-byte chunk c (8 keys) of Vt tile row d (8 chunks a row),
-// XOR-swizzled by d % 8
-__device__ __forceinline__ uint32_t fa_vswz(int d, int c) { return (uint32_t)(d * 128 + ((c ^ (d & 7)) << 4)); }
+// XOR-swizzled by d / 2 % 8.  A 16-byte read is served 16 lanes (256 bytes, every
+// bank once) at a time: rows d and d + 1 lie in different halves of the banks, so
+// the 16 rows of such a group meet in distinct bank groups (swizzling by d % 8 puts
+// rows d and d + 8 on the same banks: 4 conflict cycles a read, measured)
+__device__ __forceinline__ uint32_t fa_vswz(int d, int c) { return (uint32_t)(d * 128 + ((c ^ ((d >> 1) & 7)) << 4)); }
 
 __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
@@ -134,7 +137,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         for (int qq = 0; qq < 4; ++qq) {
             const int qi = 4 * w + qq;
             const int d = 8 * qi + (lane >> 3);
-            const int c = (lane & 7) ^ (d & 7);
+            const int c = (lane & 7) ^ ((d >> 1) & 7);
             // T_cap is a multiple of 32, so only chunks wholly past the capacity clamp
             const int k0 = min(kb + 8 * c, a.T_cap - 8);
             dma::dma16(vbase + (size_t)d * a.T_cap + k0, vl + 1024 * qi);
@@ -156,13 +159,16 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     __syncthreads();
     const float sc = a.scale_log2;
     const int arow = fa_swap23(li);                    // key row of operand A in each 32-key half
-    auto block = [&](int blk, auto mask_tag) {
+    // the stage is a compile-time constant in each copy of the body, so that every
+    // operand read is a loop-invariant lane offset plus an immediate
+    auto block = [&](int blk, auto mask_tag, auto stage_tag) {
         constexpr bool MASK = decltype(mask_tag)::value;
-        const int kb = blk * FA_KB, st = blk % FA_NST;
+        constexpr int st = decltype(stage_tag)::value;
+        const int kb = blk * FA_KB;
         const uint8_t *K = smem + st * FA_STAGE;
         const uint8_t *V = K + FA_KTILE;
         // block blk + 1 goes to the stage block blk - 1 used (read before the last barrier)
-        if (blk + 1 < nblk) stage_blk(kb + FA_KB, (blk + 1) % FA_NST);
+        if (blk + 1 < nblk) stage_blk(kb + FA_KB, st ^ 1);
         // S^T for the block's two 32-key halves: register r of sacc[kh] is key
         // kb + 32 kh + 16 (r / 8) + 8 lh + r % 8
         f32x16_t sacc[2];
@@ -246,9 +252,19 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         __syncthreads();
     };
     // the blocks below every column's limit of this wave, then those that need the mask
-    // (each wave runs nblk blocks, one barrier each)
-    for (int blk = 0; blk < nfull; ++blk) block(blk, std::false_type{});
-    for (int blk = nfull; blk < nblk; ++blk) block(blk, std::true_type{});
+    // (each wave runs nblk blocks, one barrier each); block blk is in stage blk % 2
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    int blk = 0;
+    for (; blk + 1 < nfull; blk += 2) {
+        block(blk, std::false_type{}, S0{});
+        block(blk + 1, std::false_type{}, S1{});
+    }
+    if (blk < nfull) block(blk++, std::false_type{}, S0{});
+    for (; blk < nblk; ++blk) {
+        if (blk & 1) block(blk, std::true_type{}, S1{});
+        else block(blk, std::true_type{}, S0{});
+    }
     const float ltot = lsum + __shfl_xor(lsum, 32);
     if (!col_ok) return;
     const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
