@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 9
+#define SC_ABI_VERSION 10
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
@@ -249,6 +249,23 @@ int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cac
                       int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
                       int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, void *workspace,
                       int64_t workspace_bytes, void *hip_stream);
+
+/*
+ * sc_attention_bf16 with an additive mask: scores q k^T * scale + mask[b, h, s, t]
+ * + causal mask, softmax, times v.  Mask element (b, h, s, t) (q head h, new
+ * position s, key t of the cache_len[0] + S keys) is the fp32 at mask + b*mask_stride_b
+ * + h*mask_stride_h + s*mask_stride_s + t*mask_stride_t; strides are in elements and
+ * non-negative, 0 broadcasting a dimension, and the caller sizes the mask for every
+ * key t a position sees.  A row whose visible scores are all -inf gives NaN, as the
+ * reference's softmax does.  Workspace as for sc_attention_bf16.  Replaces
+ * attention.py:449-450 (attn_scores + attention_mask) together with the steps
+ * sc_attention_bf16 replaces (src/shardcompute/parallel/attention.py:437-466).
+ */
+int sc_attention_masked_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache, const uint16_t *v_cache_t,
+                             int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
+                             int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, const float *mask,
+                             int64_t mask_stride_b, int64_t mask_stride_h, int64_t mask_stride_s,
+                             int64_t mask_stride_t, void *workspace, int64_t workspace_bytes, void *hip_stream);
 
 /* Bytes of workspace sc_attention_decode_bf16 needs (0: none). */
 int64_t sc_attention_decode_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap);

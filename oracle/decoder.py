@@ -135,14 +135,18 @@ def silu(x32):
         return x / (np.float32(1) + np.exp(-x, dtype=np.float32))
 
 
-def attention_core(q, k, v, scale, causal_offset):
+def attention_core(q, k, v, scale, causal_offset, mask=None):
     """q [B,H,S,D]; k,v [B,H,T,D] (already GQA-expanded) -> [B,H,S,D] bf16-valued.
 
     Query row i may attend to key j iff ``j <= i + causal_offset`` (with
     ``causal_offset = T - S`` this is the reference's ``triu(k = T - S + 1)``).
+    ``mask``: an additive mask broadcastable to [B,H,S,T], added to the scaled
+    scores before the causal mask (``parallel/attention.py:447-458``).
     """
     s = np.einsum("bhsd,bhtd->bhst", q.astype(np.float32), k.astype(np.float32),
                   dtype=np.float32) * np.float32(scale)
+    if mask is not None:
+        s = s + np.asarray(mask, np.float32)
     S, T = s.shape[-2], s.shape[-1]
     if S > 1:
         i = np.arange(S)[:, None]
@@ -171,7 +175,7 @@ class OracleDecoder:
     def reset(self):
         self.cache = [None] * self.shape.num_layers
 
-    def _attn(self, li, x, L):
+    def _attn(self, li, x, L, mask=None):
         sh = self.shape
         B, S, _ = x.shape
         D, H, Hk = sh.head_dim, sh.num_heads, sh.num_kv_heads
@@ -190,7 +194,7 @@ class OracleDecoder:
         rep = H // Hk
         kk = np.repeat(k, rep, axis=1)
         vv = np.repeat(v, rep, axis=1)
-        o = attention_core(q, kk, vv, 1.0 / np.sqrt(D), k.shape[2] - S)
+        o = attention_core(q, kk, vv, 1.0 / np.sqrt(D), k.shape[2] - S, mask=mask)
         o = o.transpose(0, 2, 1, 3).reshape(B, S, H * D)
         return qlinear(o, L["o"], sh)
 
@@ -201,14 +205,16 @@ class OracleDecoder:
         a = round_bf16(silu(g) * u)
         return qlinear(a, L["down"], sh)
 
-    def forward(self, ids, last_only=False):
-        """ids int [B, S] -> logits bf16-valued fp32 [B, S or 1, V]; updates the cache."""
+    def forward(self, ids, last_only=False, mask=None):
+        """ids int [B, S] -> logits bf16-valued fp32 [B, S or 1, V]; updates the cache.
+        ``mask``: the additive attention mask every layer adds to its scores
+        (``transformer.py:548-553``)."""
         sh = self.shape
         ids = np.asarray(ids)
         h = bf16_to_f32(vocab_gather_bf16(ids, self.w["embed"], 0))
         for li, L in enumerate(self.w["layers"]):
             xn = rms_norm(h, L["input_ln"], sh.rms_norm_eps)
-            h = round_bf16(h + self._attn(li, xn, L))
+            h = round_bf16(h + self._attn(li, xn, L, mask=mask))
             xn = rms_norm(h, L["post_ln"], sh.rms_norm_eps)
             h = round_bf16(h + self._mlp(xn, L))
         if last_only:

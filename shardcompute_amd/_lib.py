@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -35,6 +35,7 @@ EXPORTS = (
     "sc_rope_append_kv_bf16",
     "sc_attention_workspace_bytes",
     "sc_attention_bf16",
+    "sc_attention_masked_bf16",
     "sc_attention_decode_workspace_bytes",
     "sc_attention_decode_bf16",
     "sc_silu_mul_bf16",
@@ -105,6 +106,9 @@ def load():
         lib.sc_attention_workspace_bytes.restype = i64
         lib.sc_attention_bf16.argtypes = [p, i64, p, p, i64, p, p, i64, i64, i64, i64, i64, i64, f32, p, i64, p]
         lib.sc_attention_bf16.restype = i32
+        lib.sc_attention_masked_bf16.argtypes = [p, i64, p, p, i64, p, p, i64, i64, i64, i64, i64, i64, f32, p,
+                                                 i64, i64, i64, i64, p, i64, p]
+        lib.sc_attention_masked_bf16.restype = i32
         lib.sc_attention_decode_workspace_bytes.argtypes = [i64, i64, i64, i64, i64]
         lib.sc_attention_decode_workspace_bytes.restype = i64
         lib.sc_attention_decode_bf16.argtypes = [p, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, f32, p,
@@ -497,12 +501,17 @@ def attention_workspace_bytes(B, S, H, Hkv, D, T_cap):
     return int(load().sc_attention_workspace_bytes(B, S, H, Hkv, D, T_cap))
 
 
-def attention(q, B, S, H, Hkv, D, k_cache, v_cache_t, cache_len, scale, out=None, workspace=None):
+def attention(q, B, S, H, Hkv, D, k_cache, v_cache_t, cache_len, scale, out=None, workspace=None, mask=None,
+              n_keys=None):
     """Causal GQA attention of the S new positions (rows of q [B*S, >= H*D]) against
     the cache: cache_len[0] earlier positions followed by the S new ones.
-    Returns out [B*S, H*D] bf16."""
+    Returns out [B*S, H*D] bf16.
+
+    ``mask``: an additive mask broadcastable to ``[B, H, S, n_keys]`` (``n_keys`` =
+    cache_len[0] + S, which the caller states: the length is a device counter),
+    added to the scaled scores before the causal mask (``attention.py:449-450``)."""
     lib = load()
-    _require_gpu(q, k_cache, v_cache_t, cache_len, out, workspace)
+    _require_gpu(q, k_cache, v_cache_t, cache_len, out, workspace, mask)
     _bf16(q, "q"), _i32(cache_len, "cache_len")
     if q.dim() != 2 or q.shape[0] != B * S or q.stride(1) != 1:
         raise ValueError(f"q must be a row-major [{B * S}, *] matrix")
@@ -513,11 +522,38 @@ def attention(q, B, S, H, Hkv, D, k_cache, v_cache_t, cache_len, scale, out=None
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    rc = lib.sc_attention_bf16(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
-                               _ptr(out), out.stride(0), B, S, H, Hkv, D, float(scale), _ptr(workspace), ws_bytes,
-                               _stream(q))
-    _check(rc, "sc_attention_bf16")
+    if mask is None:
+        rc = lib.sc_attention_bf16(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
+                                   _ptr(out), out.stride(0), B, S, H, Hkv, D, float(scale), _ptr(workspace),
+                                   ws_bytes, _stream(q))
+        _check(rc, "sc_attention_bf16")
+        return out
+    m = broadcast_mask(mask, B, H, S, n_keys)
+    rc = lib.sc_attention_masked_bf16(_ptr(q), q.stride(0), _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
+                                      _ptr(out), out.stride(0), B, S, H, Hkv, D, float(scale), _ptr(m), *m.stride(),
+                                      _ptr(workspace), ws_bytes, _stream(q))
+    _check(rc, "sc_attention_masked_bf16")
     return out
+
+
+def broadcast_mask(mask, B, H, S, n_keys):
+    """An additive attention mask as an fp32 view of shape ``[B, H, S, n_keys]`` whose
+    broadcast dimensions have stride 0 (the layout sc_attention_masked_bf16 reads).
+    Raises ValueError when the mask does not broadcast to that shape."""
+    if n_keys is None:
+        raise ValueError("a masked attention call needs n_keys (cache length + S)")
+    if not isinstance(mask, torch.Tensor):
+        raise TypeError("attention mask must be a torch tensor on the GPU")
+    m = mask if mask.dtype == torch.float32 else mask.float()
+    if m.dim() > 4:
+        raise ValueError(f"attention mask has {m.dim()} dimensions (at most 4)")
+    while m.dim() < 4:
+        m = m.unsqueeze(0)
+    try:
+        return torch.broadcast_to(m, (B, H, S, n_keys))
+    except RuntimeError as e:
+        raise ValueError(f"attention mask of shape {tuple(mask.shape)} does not broadcast to "
+                         f"[{B}, {H}, {S}, {n_keys}]") from e
 
 
 def attention_decode_workspace_bytes(B, H, Hkv, D, T_cap):

@@ -45,7 +45,8 @@ int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H
                             long out_stride, void *workspace, long workspace_bytes, hipStream_t stream);
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
-                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream);
+                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream,
+                     const float *mask, const long *mask_strides);
 int launch_silu_mul(const uint16_t *gu, long rows, long I, uint16_t *out, hipStream_t stream);
 int launch_argmax(const uint16_t *logits, long rows, long V, int32_t *ids, int32_t *tokens, long tok_stride,
                   long tok_cols, const int32_t *step, hipStream_t stream);
@@ -353,7 +354,19 @@ int sc_attention_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cac
                       int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, void *workspace,
                       int64_t workspace_bytes, void *hip_stream) {
     return launch_attention(q, q_stride, k_cache, v_cache_t, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
-                            scale, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(hip_stream));
+                            scale, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(hip_stream), nullptr,
+                            nullptr);
+}
+
+int sc_attention_masked_bf16(const uint16_t *q, int64_t q_stride, const uint16_t *k_cache, const uint16_t *v_cache_t,
+                             int64_t T_cap, const int32_t *cache_len, uint16_t *out, int64_t out_stride, int64_t B,
+                             int64_t S, int64_t H, int64_t Hkv, int64_t D, float scale, const float *mask,
+                             int64_t mask_stride_b, int64_t mask_stride_h, int64_t mask_stride_s,
+                             int64_t mask_stride_t, void *workspace, int64_t workspace_bytes, void *hip_stream) {
+    if (!mask) return set_error(SC_EINVAL, "attention_masked: null mask");
+    const long ms[4] = {mask_stride_b, mask_stride_h, mask_stride_s, mask_stride_t};
+    return launch_attention(q, q_stride, k_cache, v_cache_t, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
+                            scale, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(hip_stream), mask, ms);
 }
 
 int64_t sc_attention_decode_workspace_bytes(int64_t B, int64_t H, int64_t Hkv, int64_t D, int64_t T_cap) {

@@ -145,6 +145,8 @@ struct AttnArgs {
     uint16_t *out;
     long out_stride;
     float *part;             // [B, H, S, nsplit, D + 4] when nsplit > 1: o[D], m, l, pad
+    const float *mask;       // additive mask, element (b, h, s, t) at b*msb + h*msh + s*mss + t*mst
+    long msb, msh, mss, mst;
     int B, S, H, Hkv, T_cap;
     int R, Rc, Pw, hgroups, npb;
     int kps, nsplit;
@@ -182,9 +184,12 @@ __device__ __forceinline__ void attn_load(AttnBlock<D> &blk, const uint16_t *kba
 // S^T, masked online softmax and O^T update for one block of 32 keys.  Cache slots
 // at or past vend may hold anything, NaN included: in the block that reaches them
 // their V pieces are zeroed, so that their zero probabilities meet no NaN.
-template <int D>
+// With MASKED, mrow[key * mst] (the column's row of the additive mask) is added to
+// each score the column may see (attention.py:449-450: scores * scale + mask).
+template <int D, bool MASKED = false>
 __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8_t *qv, int kb, int limit, int vend,
-                                           int g, float scale_log2, float &m, float &lsum, f4 *o) {
+                                           int g, float scale_log2, float &m, float &lsum, f4 *o,
+                                           const float *mrow = nullptr, long mst = 0) {
     f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < D / 32; ++u) {
@@ -196,6 +201,14 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
     for (int r = 0; r < 4; ++r) {
         sv[r] = (kb + 4 * g + r <= limit) ? s0[r] * scale_log2 : -INFINITY;
         sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * scale_log2 : -INFINITY;
+    }
+    if (MASKED) {
+        constexpr float LOG2E = 1.4426950408889634f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int key = kb + 16 * (r >> 2) + 4 * g + (r & 3);
+            if (key <= limit) sv[r] += mrow[(long)key * mst] * LOG2E;
+        }
     }
     float bm = sv[0];
 #pragma unroll
@@ -238,7 +251,7 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
 // range's 32-key blocks round-robin (next block prefetched while one is computed),
 // then merge their (m, l, O) through LDS.  With one key range the merged result is
 // the output; with several it is a partial for attn_combine_kernel.
-template <int D>
+template <int D, bool MASKED>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
     constexpr int U = D / 32;
     constexpr int DT = D / 16;
@@ -270,6 +283,7 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
     int pos, h;
     const bool col_ok = col_info(c, pos, h);
     const int limit = col_ok ? min(pos + off, T - 1) : -1;   // last key this column may see
+    const float *mrow = MASKED && col_ok ? a.mask + b * a.msb + h * a.msh + pos * a.mss : nullptr;
 
     bf16x8_t qv[U];
 #pragma unroll
@@ -297,11 +311,11 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_kernel(AttnArgs a) {
     while (true) {
         const int kn = kb + ATTN_STRIDE;
         attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
-        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T, g, a.scale_log2, m, lsum, o);
+        if (kb < k_hi) attn_block<D, MASKED>(cur, qv, kb, limit, T, g, a.scale_log2, m, lsum, o, mrow, a.mst);
         if (kn >= k_hi) break;
         const int kn2 = kn + ATTN_STRIDE;
         attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
-        attn_block<D>(nxt, qv, kn, limit, T, g, a.scale_log2, m, lsum, o);
+        attn_block<D, MASKED>(nxt, qv, kn, limit, T, g, a.scale_log2, m, lsum, o, mrow, a.mst);
         if (kn2 >= k_hi) break;
         kb = kn2;
     }
@@ -782,6 +796,7 @@ struct AttnPlan {
 
 void plan_attention(long B, long S, long H, long Hkv, long D, long T_cap, AttnPlan *pl) {
     AttnArgs &a = pl->a;
+    a = AttnArgs{};
     a.B = (int)B; a.S = (int)S; a.H = (int)H; a.Hkv = (int)Hkv; a.T_cap = (int)T_cap;
     a.R = (int)(H / Hkv);
     a.Rc = a.R < 16 ? a.R : 16;
@@ -921,9 +936,12 @@ int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, co
                         const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
                         long D, float scale, hipStream_t stream);
 
+// mask (optional): the additive mask of sc_attention_masked_bf16, element (b, h, s, t)
+// at mask + b*ms[0] + h*ms[1] + s*ms[2] + t*ms[3]; a masked call runs attn_kernel.
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
-                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream) {
+                     long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream,
+                     const float *mask, const long *ms) {
     if (!q || !kc || !vt || !cache_len || !out) return set_error(SC_EINVAL, "attention: null pointer");
     if (D != 64 && D != 128) return set_error(SC_EUNSUPPORTED, "attention: head_dim %ld (64 or 128 supported)", D);
     if (B <= 0 || S <= 0 || H <= 0 || Hkv <= 0 || H % Hkv)
@@ -933,11 +951,15 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
         return set_error(SC_EINVAL, "attention: bad row strides");
     if (((uintptr_t)q | (uintptr_t)kc) % 16 || ((uintptr_t)vt | (uintptr_t)out) % 8)
         return set_error(SC_EINVAL, "attention: misaligned pointers");
+    if (mask && (!ms || ms[0] < 0 || ms[1] < 0 || ms[2] < 0 || ms[3] < 0))
+        return set_error(SC_EINVAL, "attention: mask strides must be given and non-negative");
     // many positions: attn_prefill_kernel (attn_prefill.hip, 128 columns a workgroup)
     // when the shape suits it; otherwise attn_kernel, which can also split the keys
-    const int pf = launch_attn_prefill(q, q_stride, kc, vt, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
-                                       scale, stream);
-    if (pf <= 0) return pf;
+    if (!mask) {
+        const int pf = launch_attn_prefill(q, q_stride, kc, vt, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
+                                           scale, stream);
+        if (pf <= 0) return pf;
+    }
     AttnPlan pl;
     plan_attention(B, S, H, Hkv, D, T_cap, &pl);
     AttnArgs a = pl.a;
@@ -945,6 +967,8 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
     a.out = out; a.out_stride = out_stride;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.part = nullptr;
+    a.mask = mask;
+    a.msb = mask ? ms[0] : 0; a.msh = mask ? ms[1] : 0; a.mss = mask ? ms[2] : 0; a.mst = mask ? ms[3] : 0;
     if (a.nsplit > 1) {
         const long need = B * H * S * (long)a.nsplit * (D + 4) * (long)sizeof(float);
         if (!workspace || workspace_bytes < need)
@@ -953,8 +977,14 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
         a.part = static_cast<float *>(workspace);
     }
     const unsigned blocks = (unsigned)pl.blocks;
-    if (D == 128) hipLaunchKernelGGL(attn_kernel<128>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
-    else hipLaunchKernelGGL(attn_kernel<64>, dim3(blocks), dim3(64 * ATTN_WAVES), 0, stream, a);
+    const dim3 grid(blocks), wg(64 * ATTN_WAVES);
+    if (mask) {
+        if (D == 128) hipLaunchKernelGGL((attn_kernel<128, true>), grid, wg, 0, stream, a);
+        else hipLaunchKernelGGL((attn_kernel<64, true>), grid, wg, 0, stream, a);
+    } else {
+        if (D == 128) hipLaunchKernelGGL((attn_kernel<128, false>), grid, wg, 0, stream, a);
+        else hipLaunchKernelGGL((attn_kernel<64, false>), grid, wg, 0, stream, a);
+    }
     SC_HIP_CHECK(hipGetLastError());
     if (a.nsplit > 1) {
         const unsigned cb = (unsigned)((B * H * S + 3) / 4);

@@ -158,25 +158,28 @@ class ParallelAttention:
     def qkv_width(self):
         return (self.local_num_heads + 2 * self.local_num_kv_heads) * self.head_dim
 
-    def attend(self, x2, B, S, kv: LayerKV, out=None, qkv_out=None, workspace=None, pos_offset=0):
+    def attend(self, x2, B, S, kv: LayerKV, out=None, qkv_out=None, workspace=None, pos_offset=0, mask=None):
         """Core of the forward: x2 ``[B*S, hidden]`` -> attention output ``[B*S, local_hidden]``
         (before o_proj), appending the S new positions at ``kv.counters[0]``."""
         return self.attend_qkv(self.qkv(x2, out=qkv_out), B, S, kv, out=out, workspace=workspace,
-                               pos_offset=pos_offset)
+                               pos_offset=pos_offset, mask=mask)
 
-    def attend_qkv(self, qkv, B, S, kv: LayerKV, out=None, workspace=None, pos_offset=0):
+    def attend_qkv(self, qkv, B, S, kv: LayerKV, out=None, workspace=None, pos_offset=0, mask=None):
         """RoPE, cache append and attention on an already computed q|k|v product.
 
         One position per sequence (decode) runs as the fused decode attention
-        (RoPE, append and attention in one launch, plus the range merge)."""
+        (RoPE, append and attention in one launch, plus the range merge).  ``mask``
+        is the reference's additive ``attention_mask``, broadcastable to
+        ``[B, local heads, S, cached + S keys]`` (``attention.py:449-450``)."""
         H, Hk, D = self.local_num_heads, self.local_num_kv_heads, self.head_dim
         cos_t, sin_t = self.rope.tables(kv.cache.capacity + pos_offset, qkv.device)
-        if S == 1 and H // Hk <= 16:
+        if S == 1 and H // Hk <= 16 and mask is None:
             return _lib.attention_decode(qkv, B, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, self.scale,
                                          pos_offset=pos_offset, out=out, workspace=workspace)
+        n_keys = kv.length + S
         _lib.rope_append_kv(qkv, B, S, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, pos_offset=pos_offset)
         return _lib.attention(qkv, B, S, H, Hk, D, kv.k, kv.vt, kv.counters, self.scale, out=out,
-                              workspace=workspace)
+                              workspace=workspace, mask=mask, n_keys=n_keys)
 
     def _prepare_cache(self, past_key_value, B, S, device):
         """-> (LayerKV, temp cache or None, whether to return a tuple)."""
@@ -189,17 +192,11 @@ class ParallelAttention:
             tmp.load_tuples([past_key_value])
         return tmp[0], tmp
 
-    def _check_mask(self, attention_mask):
-        if attention_mask is not None:
-            raise NotImplementedError("additive attention_mask is not supported by the HIP attention kernel "
-                                      "(the causal mask is built in)")
-
     def _attn_core(self, hidden_states, attention_mask, past_key_value, use_cache):
-        self._check_mask(attention_mask)
         B, S, _ = hidden_states.shape
         x2 = hidden_states.reshape(B * S, -1)
         kv, tmp = self._prepare_cache(past_key_value, B, S, hidden_states.device)
-        a = self.attend(x2, B, S, kv)
+        a = self.attend(x2, B, S, kv, mask=attention_mask)
         if tmp is not None:
             tmp.advance(S)
             new_cache = tmp[0].as_tuple() if use_cache else None
@@ -216,11 +213,12 @@ class ParallelAttention:
     def forward_sync_partial(self, hidden_states: torch.Tensor, attention_mask=None, position_offset: int = 0):
         """Attention without all-reduce and without cache (``attention.py:473-520``):
         the S positions attend causally among themselves, rotated for
-        ``position_offset + s``."""
-        self._check_mask(attention_mask)
+        ``position_offset + s``; ``attention_mask`` is added to the scaled scores
+        (``attention.py:507-508``)."""
         B, S, _ = hidden_states.shape
         tmp = KVCache(1, B, self.local_num_kv_heads, self.head_dim, S, device=hidden_states.device)
-        a = self.attend(hidden_states.reshape(B * S, -1), B, S, tmp[0], pos_offset=position_offset)
+        a = self.attend(hidden_states.reshape(B * S, -1), B, S, tmp[0], pos_offset=position_offset,
+                        mask=attention_mask)
         return self.o_proj.forward_partial(a.reshape(B, S, self.local_hidden))
 
     def forward_partial_with_cache(self, hidden_states: torch.Tensor, attention_mask=None, past_key_value=None,

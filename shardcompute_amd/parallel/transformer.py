@@ -286,8 +286,9 @@ class ParallelTransformer:
                 emb = await self.communicator.all_reduce(emb, op="sum")
         return emb
 
-    async def _trunk(self, h, cache: KVCache, B: int, S: int, bufs: Optional[StepBuffers] = None):
-        """Residual stream ``h [B*S, hidden]`` through every layer.
+    async def _trunk(self, h, cache: KVCache, B: int, S: int, bufs: Optional[StepBuffers] = None, mask=None):
+        """Residual stream ``h [B*S, hidden]`` through every layer (``mask``: the
+        additive attention mask every layer's attention adds to its scores).
 
         Each RMSNorm (with the residual add before it) runs inside the projection
         that reads it, and the SiLU gate inside down_proj.  The residual stream
@@ -304,7 +305,7 @@ class ParallelTransformer:
             if pending is not None:
                 h, h_alt = h_alt, h
             a = att.attend_qkv(qkv, B, S, cache[i], out=bufs.attn if bufs else None,
-                               workspace=bufs.workspace if bufs else None)
+                               workspace=bufs.workspace if bufs else None, mask=mask)
             o = await att.o_proj.forward(a)
             mlp._check_supported()
             act = mlp.gate_up.swiglu_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
@@ -353,9 +354,9 @@ class ParallelTransformer:
 
         ``past_key_values``: a :class:`KVCache` (appended in place, returned as is),
         a list of reference-layout ``(k, v)`` tuples (the grown list is returned),
-        or ``None``."""
-        if attention_mask is not None:
-            raise NotImplementedError("additive attention_mask is not supported by the HIP attention kernel")
+        or ``None``.  ``attention_mask``: an additive mask broadcastable to
+        ``[batch, local heads, seq, cached + seq keys]``, passed to every layer
+        (``transformer.py:548-553``)."""
         ids = input_ids if isinstance(input_ids, torch.Tensor) else torch.as_tensor(input_ids)
         ids = ids.to(self.device)
         if ids.dim() != 2:
@@ -370,7 +371,7 @@ class ParallelTransformer:
                 cache.load_tuples(past_key_values)
         cache.check_room(S)
         h = (await self._embed(ids)).reshape(B * S, self.hidden_size).contiguous()
-        h, pending = await self._trunk(h, cache, B, S)
+        h, pending = await self._trunk(h, cache, B, S, mask=attention_mask)
         logits = await self._head(h, pending, B, S, last_only)
         cache.advance(S)
         new_cache = (cache.as_tuples() if tuples else cache) if use_cache else None

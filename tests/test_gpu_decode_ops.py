@@ -177,6 +177,66 @@ def test_attention_nan_past_length(device, B, S, H, Hkv, D, past, extra):
     assert np.isfinite(err) and err <= ATTN_TOL
 
 
+def _mask_for(rng, kind, B, H, S, T):
+    """An additive mask of the named layout, key 0 always visible (finite rows)."""
+    if kind == "pad":                       # [B, 1, 1, T]: some keys hidden per sequence
+        m = np.zeros((B, 1, 1, T), np.float32)
+        for b in range(B):
+            hide = rng.choice(np.arange(1, T), size=max(1, T // 5), replace=False)
+            m[b, 0, 0, hide] = -np.inf
+        return m
+    if kind == "full":                      # [B, H, S, T]
+        m = rng.standard_normal((B, H, S, T)).astype(np.float32) * 2
+        m[..., 1::7] = -np.inf
+        return m
+    if kind == "rowcol":                    # [S, T]: leading dimensions broadcast
+        return (rng.standard_normal((S, T)) * 1.5).astype(np.float32)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("B,S,H,Hkv,D,past,extra,kind", [
+    (2, 64, 32, 8, 128, 0, 0, "pad"),       # a prefill the 128-column kernel would take unmasked
+    (1, 48, 8, 2, 64, 100, 30, "full"),     # head_dim 64, after a cache
+    (1, 1, 32, 8, 128, 2047, 256, "pad"),   # one position, keys split over workgroups
+    (3, 1, 8, 1, 128, 300, 0, "full"),      # one position, 8 heads per KV head
+    (1, 200, 32, 8, 128, 0, 40, "rowcol"),
+])
+def test_attention_additive_mask(device, B, S, H, Hkv, D, past, extra, kind):
+    rng = np.random.default_rng(B + S + past)
+    T = past + S
+    T_cap = ((T + extra + 31) // 32) * 32
+    q = _bf(rng, (B * S, H * D))
+    k = _bf(rng, (B, Hkv, T_cap, D))
+    v = _bf(rng, (B, Hkv, T_cap, D))
+    m = _mask_for(rng, kind, B, H, S, T)
+    cnt = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    print(f"attention with a {kind} mask {m.shape}: B={B} S={S} H={H} Hkv={Hkv} D={D} past={past}", flush=True)
+    out = _lib.attention(dev_bf16(q), B, S, H, Hkv, D, dev_bf16(k),
+                         dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2))), cnt, 1.0 / np.sqrt(D),
+                         mask=torch.from_numpy(m).cuda(), n_keys=T)
+    torch.cuda.synchronize()
+    rep = H // Hkv
+    q4 = bf16_to_f32(q).reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    kk = np.repeat(bf16_to_f32(k[:, :, :T]), rep, axis=1)
+    vv = np.repeat(bf16_to_f32(v[:, :, :T]), rep, axis=1)
+    ref = attention_core(q4, kk, vv, 1.0 / np.sqrt(D), T - S, mask=m).transpose(0, 2, 1, 3).reshape(B * S, H * D)
+    got = bf16_to_f32(host_u16(out))
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= ATTN_TOL
+
+
+def test_attention_mask_errors(device):
+    q = torch.zeros((4, 256), dtype=torch.bfloat16, device="cuda")
+    kc = torch.zeros((1, 2, 32, 128), dtype=torch.bfloat16, device="cuda")
+    vt = torch.zeros((1, 2, 128, 32), dtype=torch.bfloat16, device="cuda")
+    cnt = torch.zeros(2, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="does not broadcast"):
+        _lib.attention(q, 1, 4, 2, 2, 128, kc, vt, cnt, 0.1, mask=torch.zeros((1, 3, 4, 4), device="cuda"),
+                       n_keys=4)
+    with pytest.raises(ValueError, match="n_keys"):
+        _lib.attention(q, 1, 4, 2, 2, 128, kc, vt, cnt, 0.1, mask=torch.zeros((4, 4), device="cuda"))
+
+
 def _decode_case(rng, B, H, Hkv, D, past, T_cap, offset=0, base=500000.0):
     width = (H + 2 * Hkv) * D + 40                  # row stride wider than the heads
     rows = _bf(rng, (B, width))

@@ -190,6 +190,24 @@ def test_block_api_matches_oracle(device, weights, model):
     assert cache[0].shape == (1, SHAPE.num_kv_heads, 6, SHAPE.head_dim)
 
 
+def test_prefill_with_additive_mask(device, weights, model):
+    # the reference's attention_mask, added by every layer to its scaled scores
+    # (transformer.py:548-553, attention.py:449-450), against the oracle
+    rng = np.random.default_rng(21)
+    B, S = 2, 9
+    ids = rng.integers(0, SHAPE.vocab_size, (B, S))
+    m = (rng.standard_normal((B, 1, S, S)) * 2).astype(np.float32)
+    m[0, 0, :, 3] = -np.inf
+    m[1, 0, 5:, 1:4] = -np.inf
+    logits, _ = run(model.forward(torch.from_numpy(ids).cuda(), attention_mask=torch.from_numpy(m).cuda()))
+    ref = OracleDecoder(SHAPE, weights).forward(ids, mask=m)
+    assert rel(logits_np(logits), ref) <= LOGIT_TOL
+    # a zero mask (the masked kernel) equals no mask
+    z, _ = run(model.forward(torch.from_numpy(ids).cuda(), attention_mask=torch.zeros((1, 1, 1, S), device="cuda")))
+    plain, _ = run(model.forward(torch.from_numpy(ids).cuda()))
+    assert rel(logits_np(z), logits_np(plain)) <= 1e-2
+
+
 def test_attention_forward_sync_partial(device, weights, model):
     # cache-less attention rotated for positions offset..offset+S-1 equals the cached
     # path when the cache starts at that offset with no earlier keys visible only if

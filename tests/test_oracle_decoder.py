@@ -286,3 +286,46 @@ def test_attention_causal_uniform_scores():
     dec = OracleDecoder(sh, dict(layers=[L]))
     inc = np.concatenate([dec._attn(0, x[:, t:t + 1], L)[0] for t in range(6)])
     assert _close(inc, exp, 1e-2)
+
+
+def _mask_case(seed, T=9, D=8):
+    rng = np.random.default_rng(seed)
+    q = round_bf16(rng.standard_normal((1, 2, 1, D)).astype(np.float32))
+    k = round_bf16(rng.standard_normal((1, 2, T, D)).astype(np.float32))
+    v = round_bf16(rng.standard_normal((1, 2, T, D)).astype(np.float32))
+    return q, k, v
+
+
+def test_attention_mask_zero_and_row_constant_are_no_ops():
+    # softmax is invariant to a per-row shift: a mask constant along the keys changes
+    # nothing (a mask applied after the softmax, or multiplied in, would)
+    q, k, v = _mask_case(2)
+    base = attention_core(q, k, v, 0.35, k.shape[2] - 1)
+    assert np.array_equal(attention_core(q, k, v, 0.35, k.shape[2] - 1, mask=np.zeros((1, 1, 1, 9))), base)
+    shifted = attention_core(q, k, v, 0.35, k.shape[2] - 1, mask=np.full((1, 2, 1, 1), -3.0))
+    assert np.allclose(shifted, base, atol=1e-6, rtol=0)
+
+
+def test_attention_mask_minus_inf_drops_the_key():
+    # -inf at key j for one position equals attending without key j
+    q, k, v = _mask_case(3)
+    j = 4
+    m = np.zeros((1, 1, 1, 9), np.float32)
+    m[..., j] = -np.inf
+    got = attention_core(q, k, v, 0.35, 8, mask=m)
+    keep = [i for i in range(9) if i != j]
+    ref = attention_core(q, k[:, :, keep], v[:, :, keep], 0.35, 7)
+    assert np.allclose(got, ref, atol=1e-6, rtol=0)
+
+
+def test_attention_mask_log2_doubles_a_key():
+    # adding log 2 to key j's scaled score equals key j appearing twice (a mask scaled
+    # with the scores, or subtracted, would not)
+    q, k, v = _mask_case(4)
+    j = 2
+    m = np.zeros((1, 1, 1, 9), np.float32)
+    m[..., j] = np.log(2.0)
+    got = attention_core(q, k, v, 0.35, 8, mask=m)
+    dup = [0, 1, 2, 2, 3, 4, 5, 6, 7, 8]
+    ref = attention_core(q, k[:, :, dup], v[:, :, dup], 0.35, 9)
+    assert np.allclose(got, ref, atol=1e-6, rtol=0)

@@ -59,8 +59,16 @@ def test_attention_constructor_validation():
     with pytest.raises(RuntimeError):
         a2 = ParallelAttention(256, 4, 1, 0, None)
         a2.load_quantized_shards(*([None] * 16))
-    with pytest.raises(NotImplementedError):
-        a._check_mask(torch.zeros(1))
+    # the additive attention mask's broadcast view (what the masked kernel reads)
+    from shardcompute_amd._lib import broadcast_mask
+    m = broadcast_mask(torch.zeros((4, 9)), 2, 8, 4, 9)
+    assert m.shape == (2, 8, 4, 9) and m.stride() == (0, 0, 9, 1) and m.dtype == torch.float32
+    m = broadcast_mask(torch.zeros((2, 1, 1, 9), dtype=torch.bfloat16), 2, 8, 4, 9)
+    assert m.stride() == (9, 0, 0, 1) and m.dtype == torch.float32
+    with pytest.raises(ValueError, match="does not broadcast"):
+        broadcast_mask(torch.zeros((3, 9)), 2, 8, 4, 9)
+    with pytest.raises(ValueError, match="n_keys"):
+        broadcast_mask(torch.zeros((4, 9)), 2, 8, 4, None)
 
 
 def test_mlp_constructor_validation():
