@@ -84,6 +84,9 @@ def parse_args():
                    help="build the weights and run only the per-launch GEMV pass (for counter profiling)")
     p.add_argument("--gemm-only", action="store_true",
                    help="build the weights and run only the prefill quantized GEMM timing (for counter profiling)")
+    p.add_argument("--attn-only", action="store_true",
+                   help="run only the prefill attention of the Llama-3-8B heads at --prefill positions "
+                        "(random q, k, v; for counter profiling)")
     p.add_argument("--trunk-only", action="store_true",
                    help="prefill, then only eager whole-trunk decode launches (for counter profiling)")
     p.add_argument("--trunk-timeline", action="store_true",
@@ -525,6 +528,36 @@ def bench_w8_gemv(reps):
             "frac": round(g["GBs"] / HBM_PEAK_GBS, 4), "per_shape": g["per_shape"]}
 
 
+def time_prefill_attention(cfg, B, P, reps):
+    """The prefill attention of one layer (B x P new positions, empty cache before
+    them) on random q, k, v: average launch time and TFLOP/s of the causal half."""
+    import math
+    import torch
+    from shardcompute_amd import _lib
+    H, Hkv, D = cfg["heads"], cfg["kv_heads"], cfg["hidden"] // cfg["heads"]
+    T_cap = (P + 31) // 32 * 32
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    q = torch.randn((B * P, H * D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.randn((B, Hkv, T_cap, D), generator=g, device="cuda").to(torch.bfloat16)
+    vt = torch.randn((B, Hkv, D, T_cap), generator=g, device="cuda").to(torch.bfloat16)
+    cnt = torch.zeros(2, dtype=torch.int32, device="cuda")
+    out = torch.empty((B * P, H * D), dtype=torch.bfloat16, device="cuda")
+    scale = 1.0 / math.sqrt(D)
+    _lib.attention(q, B, P, H, Hkv, D, kc, vt, cnt, scale, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        _lib.attention(q, B, P, H, Hkv, D, kc, vt, cnt, scale, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flops = 4.0 * B * H * D * P * (P + 1) / 2
+    log(f"attn-only: {B} x {P} positions, {H} q / {Hkv} kv heads of {D}: {us:.1f} us per launch, "
+        f"{flops / us / 1e6:.0f} TFLOP/s (causal half), {reps} launches")
+
+
 def timed_prefill(model, ids, cache):
     """Seconds of the prefill forward of ``ids`` into ``cache`` (last position's
     logits), after one untimed prefill of the same shape into a scratch cache (the
@@ -642,6 +675,9 @@ def main():
     _lib.load()
     cfg = dict(LLAMA3_8B)
     B, P, K, W = args.batch, args.prefill, args.steps, args.warmup
+    if args.attn_only:
+        time_prefill_attention(cfg, B, P, args.kernel_reps)
+        return
     capacity = P + W + K + 8
     t_build = time.perf_counter()
     model = build_model(cfg, args.layers, args.bits, capacity)

@@ -42,7 +42,8 @@ namespace {
 // * cache slots past the length may hold anything, NaN included: their scores are
 //   masked and, in the block that crosses the length, their V pieces are zeroed
 //   before they meet the zero probabilities;
-// * workgroups of later positions (more keys) are dispatched first.
+// * workgroups of later positions (more keys) are dispatched first, the first two
+//   rounds in heavy/light pairs.
 // The result is bf16(O / l) per column, as attn_kernel writes it (P in bf16, fp32
 // sums), with the sums in another order.
 constexpr int FA_COLS = 128, FA_KB = 64, FA_D = 128, FA_THREADS = 256;
@@ -51,6 +52,7 @@ constexpr int FA_VTILE = FA_D * FA_KB * 2;           // 16 KB: 128 dims x 128 B
 constexpr int FA_STAGE = FA_KTILE + FA_VTILE;
 constexpr int FA_NST = 2;                            // LDS stages: block blk being read, blk + 1 landing
 constexpr int FA_LDS = FA_NST * FA_STAGE;            // 64 KB
+constexpr int FA_SAHEAD = 4;                         // operand reads in flight ahead of the MFMAs
 
 struct FaArgs {
     const uint16_t *q;
@@ -61,6 +63,7 @@ struct FaArgs {
     uint16_t *out;
     long out_stride;
     int S, H, Hkv, R, T_cap, nqb;
+    int pair_half;            // > 0: the first 2 pair_half workgroups are dispatched in heavy/light pairs
     float scale_log2;
 };
 
@@ -83,9 +86,18 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int li = lane & 31, lh = lane >> 5;
-    const int qb = a.nqb - 1 - (int)(blockIdx.x % a.nqb);
-    const int hk = (int)((blockIdx.x / a.nqb) % a.Hkv);
-    const int b = (int)(blockIdx.x / ((unsigned)a.nqb * a.Hkv));
+    // work rank of this workgroup (0: most keys): later positions first, over every
+    // (sequence, kv head).  Two workgroups share a CU; the first 2 pair_half (two
+    // per CU) are resident together, workgroup p beside p + pair_half in dispatch
+    // order, so that round pairs rank j with rank 2 pair_half - 1 - j and each CU
+    // gets about the same number of key blocks (a heuristic on dispatch order: any
+    // order gives the same results)
+    int rank = (int)blockIdx.x;
+    if (a.pair_half > 0 && rank < 2 * a.pair_half && rank >= a.pair_half) rank = 3 * a.pair_half - 1 - rank;
+    const int nbh = (int)(gridDim.x / a.nqb);             // B * Hkv
+    const int qb = a.nqb - 1 - rank / nbh;
+    const int hk = rank % nbh % a.Hkv;
+    const int b = rank % nbh / a.Hkv;
     const int T = a.cache_len[0] + a.S;               // cached positions, the S new ones included
     const int off = T - a.S;
     const int PB = FA_COLS / a.R;
@@ -131,7 +143,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
             const int r = 4 * qi + (lane >> 4);
             const int c = (lane & 15) ^ (fa_swap23(r) & 15);
             const int key = min(kb + r, a.T_cap - 1);
-            dma::dma16(kbase + (size_t)key * FA_D + 8 * c, kl + 1024 * qi);
+            dma::dma16s(kbase, (uint32_t)(key * (FA_D * 2) + 16 * c), kl + 1024 * qi);
         }
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
@@ -140,7 +152,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
             const int c = (lane & 7) ^ ((d >> 1) & 7);
             // T_cap is a multiple of 32, so only chunks wholly past the capacity clamp
             const int k0 = min(kb + 8 * c, a.T_cap - 8);
-            dma::dma16(vbase + (size_t)d * a.T_cap + k0, vl + 1024 * qi);
+            dma::dma16s(vbase, (uint32_t)((d * a.T_cap + k0) * 2), vl + 1024 * qi);
         }
     };
 
@@ -171,16 +183,28 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         if (blk + 1 < nblk) stage_blk(kb + FA_KB, st ^ 1);
         // S^T for the block's two 32-key halves: register r of sacc[kh] is key
         // kb + 32 kh + 16 (r / 8) + 8 lh + r % 8
-        f32x16_t sacc[2];
+        // (the two halves' chains interleaved, so consecutive MFMAs are independent;
+        // operand reads run FA_SAHEAD ahead of their MFMAs: the scheduler, left alone,
+        // issues each read just before its MFMA and waits out the LDS latency 16 times)
+        f32x16_t sacc[2] = {f32x16_t{}, f32x16_t{}};
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-            sacc[kh] = f32x16_t{};
+        for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
+            for (int kh = 0; kh < 2; ++kh) {
                 const bf16x8_t ka = as_bf16x8(*reinterpret_cast<const uint4 *>(K + fa_kswz(32 * kh + arow, 2 * ks + lh)));
                 sacc[kh] = mfma32x32x16(ka, qv[ks], sacc[kh]);
             }
+#pragma unroll
+        for (int i = 0; i < FA_SAHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 16 - FA_SAHEAD; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
+#pragma unroll
+        for (int i = 0; i < FA_SAHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
         if (MASK) {
             const int rel = limit - kb - 8 * lh;
 #pragma unroll
@@ -222,6 +246,8 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         }
         // O^T += Vt P^T over 4 steps of 16 keys: step s4 takes registers 8 (s4 % 2) ..
         // + 7 of half s4 / 2, keys kb + 8 c .. + 7 with c = 4 (s4 / 2) + 2 (s4 % 2) + lh
+        // (operand reads FA_SAHEAD ahead of their MFMAs, as for S^T)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
             const int kh = s4 >> 1, r0 = 8 * (s4 & 1);
@@ -247,6 +273,16 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
                 o[db] = mfma32x32x16(as_bf16x8(v.x & mk.x, v.y & mk.y, v.z & mk.z, v.w & mk.w), pb, o[db]);
             }
         }
+#pragma unroll
+        for (int i = 0; i < FA_SAHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int i = 0; i < 16 - FA_SAHEAD; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < FA_SAHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_barrier(0);
         // block blk + 1 must have landed before the barrier
         dma::wait_vm<0>();
         __syncthreads();
@@ -293,6 +329,7 @@ int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, co
                         long D, float scale, hipStream_t stream) {
     const long R = H / Hkv;
     if (D != FA_D || FA_COLS % R != 0 || ((uintptr_t)vt % 16) != 0) return 1;
+    if (T_cap > (1L << 22)) return 1;    // staging offsets within one (b, kv head) slab are 32-bit
     const long nqb = (S + FA_COLS / R - 1) / (FA_COLS / R);
     const long wgs = B * Hkv * nqb;
     if (S < FA_COLS / R || wgs >= (1L << 31)) return 1;
@@ -300,6 +337,8 @@ int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, co
     f.q = q; f.q_stride = q_stride; f.kc = kc; f.vt = vt; f.cache_len = cache_len;
     f.out = out; f.out_stride = out_stride;
     f.S = (int)S; f.H = (int)H; f.Hkv = (int)Hkv; f.R = (int)R; f.T_cap = (int)T_cap; f.nqb = (int)nqb;
+    const long per_round = 2L * device_info().num_cus;     // two workgroups per CU (64 KB LDS each)
+    f.pair_half = wgs >= per_round ? (int)(per_round / 2) : 0;
     f.scale_log2 = scale * 1.4426950408889634f;
     static bool configured = false;
     if (!configured) {

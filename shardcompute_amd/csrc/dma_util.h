@@ -44,6 +44,14 @@ __device__ __forceinline__ void dma16(const void *g, uint32_t lds_base) {
                  : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_base))
                  : "memory", "m0");
 }
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit byte offset per
+// lane (the SADDR form: no 64-bit address per lane in VGPRs).
+__device__ __forceinline__ void dma16s(const void *sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :
+                 : "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // (x & mask) | magic.  VOP3 on gfx950 takes no literal and one scalar operand, so
