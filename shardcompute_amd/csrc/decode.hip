@@ -79,16 +79,17 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
 // q and k heads are rotated with the rotate-half rule x*cos + [-x2, x1]*sin
 // (attention.py:130-151) using fp32 tables; rotated q is written back in place,
 // rotated k and the raw v go to the cache.
+// v_heads: Hkv (this kernel also appends v), or 0 when v_append_kernel does.
 __global__ void __launch_bounds__(256)
 rope_append_kernel(uint16_t *__restrict__ qkv, long qkv_stride, int S, int H, int Hkv, int D,
                    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
                    uint16_t *__restrict__ kc, uint16_t *__restrict__ vt, int T_cap,
-                   const int32_t *__restrict__ cache_len, int pos_offset, int table_len) {
+                   const int32_t *__restrict__ cache_len, int pos_offset, int table_len, int v_heads) {
     // one wave per head of one token: q heads, then k heads, then v heads
     const int tok = blockIdx.x;
     const int head = blockIdx.y * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (head >= H + 2 * Hkv) return;
+    if (head >= H + Hkv + v_heads) return;
     const int b = tok / S, s = tok - (tok / S) * S;
     const int pos = cache_len[0] + s;             // cache slot
     const int rpos = pos + pos_offset;            // rotary position
@@ -118,6 +119,41 @@ rope_append_kernel(uint16_t *__restrict__ qkv, long qkv_stride, int S, int H, in
         const int hk = head - H - Hkv;
         uint16_t *vc = vt + ((size_t)b * Hkv + hk) * D * T_cap + pos;
         for (int d = lane; d < D; d += 64) vc[(size_t)d * T_cap] = hp[d];
+    }
+}
+
+// The v part of rope_append for many new positions: Vt rows are [D, T_cap], so one
+// token's values land in D different rows; a workgroup takes 64 tokens of one kv head
+// through LDS and writes each dim's 64 consecutive slots with consecutive lanes
+// (one-token-per-wave scattering makes every 2-byte store touch its own line).
+// Same slots, same values, same bounds rule as rope_append_kernel.
+constexpr int VAPP_TOK = 64;
+__global__ void __launch_bounds__(256)
+v_append_kernel(const uint16_t *__restrict__ qkv, long qkv_stride, int S, int H, int Hkv, int D,
+                uint16_t *__restrict__ vt, int T_cap, const int32_t *__restrict__ cache_len, int pos_offset,
+                int table_len) {
+    __shared__ uint32_t tile[VAPP_TOK * (128 / 2 + 1)];   // token rows of D/2 + 1 words (odd: conflict-free columns)
+    const int s0 = blockIdx.x * VAPP_TOK, hk = blockIdx.y, b = blockIdx.z;
+    const int W = D / 2 + 1, cpt = D / 8;                  // words per LDS row, uint4 per token
+    const int base = cache_len[0];
+    for (int i = threadIdx.x; i < VAPP_TOK * cpt; i += 256) {
+        const int t = i / cpt, c = i - t * cpt;
+        if (s0 + t < S) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(qkv + (size_t)(b * S + s0 + t) * qkv_stride +
+                                                             (size_t)(H + Hkv + hk) * D + 8 * c);
+            uint32_t *row = tile + t * W + 4 * c;
+            row[0] = v.x; row[1] = v.y; row[2] = v.z; row[3] = v.w;
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int s = s0 + lane, pos = base + s, rpos = pos + pos_offset;
+    if (s >= S || pos < 0 || pos >= T_cap || rpos < 0 || rpos >= table_len) return;
+    uint16_t *vc = vt + ((size_t)b * Hkv + hk) * D * T_cap + pos;
+    const int dpw = D / 4;                                 // dims per wave
+    for (int d = w * dpw; d < (w + 1) * dpw; ++d) {
+        const uint32_t word = tile[lane * W + (d >> 1)];
+        vc[(size_t)d * T_cap] = (uint16_t)((d & 1) ? (word >> 16) : (word & 0xFFFFu));
     }
 }
 
@@ -856,11 +892,21 @@ int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, l
     if (T_cap <= 0 || table_len <= 0 || pos_offset < 0 || T_cap > 0x7FFFFFFFL || table_len > 0x7FFFFFFFL ||
         pos_offset > 0x7FFFFFFFL)
         return set_error(SC_EINVAL, "rope_append: bad capacity/table/offset");
-    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(B * S), (unsigned)((H + 2 * Hkv + 3) / 4)), dim3(256), 0,
-                       stream, qkv, qkv_stride, (int)S,
+    // many positions: v through v_append_kernel (64 tokens a workgroup), when its
+    // 16-byte row loads are aligned
+    const bool tiled_v = S >= 16 && D % 8 == 0 && D <= 128 && qkv_stride % 8 == 0 && (uintptr_t)qkv % 16 == 0;
+    const int v_heads = tiled_v ? 0 : (int)Hkv;
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)(B * S), (unsigned)((H + Hkv + v_heads + 3) / 4)), dim3(256),
+                       0, stream, qkv, qkv_stride, (int)S,
                        (int)H, (int)Hkv, (int)D, cos_t, sin_t, kc, vt, (int)T_cap, cache_len, (int)pos_offset,
-                       (int)table_len);
+                       (int)table_len, v_heads);
     SC_HIP_CHECK(hipGetLastError());
+    if (tiled_v) {
+        hipLaunchKernelGGL(v_append_kernel, dim3((unsigned)((S + VAPP_TOK - 1) / VAPP_TOK), (unsigned)Hkv, (unsigned)B),
+                           dim3(256), 0, stream, qkv, qkv_stride, (int)S, (int)H, (int)Hkv, (int)D, vt, (int)T_cap,
+                           cache_len, (int)pos_offset, (int)table_len);
+        SC_HIP_CHECK(hipGetLastError());
+    }
     return SC_OK;
 }
 

@@ -78,6 +78,8 @@ def test_rms_norm_constant_rows(device):
     (2, 7, 8, 2, 64, 0, 0),
     (1, 33, 4, 4, 128, 100, 0),
     (3, 2, 8, 1, 128, 5, 1000),
+    (2, 100, 8, 2, 64, 37, 5),         # many positions: v through the 64-token transpose
+    (1, 300, 32, 8, 128, 1000, 0),
 ])
 def test_rope_append(device, B, S, H, Hkv, D, past, offset):
     rng = np.random.default_rng(B + S + H + past)
