@@ -21,7 +21,8 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
-                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
+                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
+                      int swiglu_half = 0);
 int launch_vocab_gather(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
                         int64_t D, int64_t vocab_start, uint16_t *out, hipStream_t stream);
 int launch_qembed_gather(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq, const uint16_t *s,
@@ -245,6 +246,11 @@ static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw,
     if (M > 8 && M <= 32) {
         // the 9-32-row GEMV's split-K pass applies silu(gate) * up itself
         rc = launch_qgemv16(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
+    if (M > 32) {
+        // the GEMM pairs gate and up columns in its tiles and writes act itself
+        rc = launch_qgemm_mfma(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, (int)swiglu_half);
         if (rc != SC_EUNSUPPORTED) return rc;
     }
     rc = qmm_dispatch(xin, wq, s, b, bias, gu_scratch, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);

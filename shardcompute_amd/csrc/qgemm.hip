@@ -35,6 +35,12 @@ struct GemmArgs {
     int M, N, K, G;
     int ldy;               // y's row stride (N, or wider when this launch covers a column range)
     int mt, nt, tiles;     // m-tiles, n-tiles, real tiles (the grid is padded to a multiple of 8)
+    // SwiGLU (swiglu_i = I > 0): the weight stacks gate and up ([2I, K]); the N = 2I
+    // product columns are paired, column c of the launch's range holding, per 32-block
+    // b and u = c % 32, weight row ic (u < 16, gate) or I + ic (up) with
+    // ic = (n_base + c) / 32 * 16 + u % 16; y receives act [M, I] = silu(gate) * up.
+    // (The pointers are not offset for a column range; n_base locates it.)
+    int swiglu_i, n_base;
 };
 
 namespace {
@@ -119,7 +125,12 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
 
     // ---- weights: thread -> (row wr, codes [CPT * wp, CPT * wp + CPT)) of the tile
     const int wr = tid / Gm::TPR, wp = tid % Gm::TPR;
-    const int wrow = min(n0 + wr, N - 1);
+    int wrow = min(n0 + wr, N - 1);
+    if (a.swiglu_i) {
+        const int c = a.n_base + n0 + wr, u = c & 31;
+        const int ic = min((c >> 5) * 16 + (u & 15), a.swiglu_i - 1);
+        wrow = u < 16 ? ic : a.swiglu_i + ic;
+    }
     const uint8_t *wsrc = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)wrow * ((size_t)K * BITS / 8) +
                           wp * (CPT * BITS / 8);
     const uint16_t *ssrc = a.s + (size_t)wrow * G;
@@ -294,19 +305,62 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
             }
         }
     };
-    if (m0 + BM <= M) store_tile(std::false_type{});
-    else store_tile(std::true_type{});
+    // SwiGLU: in each 32-block lanes li < 16 hold gate columns and li >= 16 the up
+    // columns of the same ic; after rounding (and the bias) one permlane16 swap gives
+    // every lane both halves of its row pair, and lanes li < 16 write the pair's first
+    // row, li >= 16 its second: bf16(silu(g) * u) of the rounded g and u, as
+    // silu_mul_kernel computes it from the rounded product
+    auto store_swiglu = [&](auto checked) {
+        constexpr bool CHK = decltype(checked)::value;
+        const int I = a.swiglu_i;
+        const bool hi = (li & 16) != 0;
+#pragma unroll
+        for (int j = 0; j < Gm::NJ; ++j) {
+            const int c = a.n_base + n0 + wn * Gm::WN + j * 32 + li;
+            const int ic = (c >> 5) * 16 + (li & 15);
+            const bool ok = ic < I;
+            const float bb = a.bias && ok ? bf2f(a.bias[hi ? I + ic : ic]) : 0.f;
+            uint16_t *yc = a.y + (size_t)mw * a.ldy + ic;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int r = 0; r < 16; r += 2) {
+                    uint32_t o = cvt_pk_bf16(acc[i][j][r], acc[i][j][r + 1]);
+                    if (a.bias) o = cvt_pk_bf16(bf2f(o & 0xFFFFu) + bb, bf2f(o >> 16) + bb);
+                    float gf, uf;                       // (gate pair, up pair) bits
+                    swap16(__uint_as_float(o), gf, uf);
+                    const uint32_t g = __float_as_uint(gf), u = __float_as_uint(uf);
+                    const int sh = hi ? 16 : 0;         // li >= 16: the second row of the pair
+                    const float act = silu_mul_f(bf2f((g >> sh) & 0xFFFFu), bf2f((u >> sh) & 0xFFFFu));
+                    const int dm = i * 32 + 8 * (r >> 2) + (r & 3) + (hi ? 1 : 0);
+                    if (ok && (!CHK || mw + dm < M)) yc[(size_t)dm * a.ldy] = (uint16_t)f2bf(act);
+                }
+            }
+        }
+    };
+    if (a.swiglu_i) {
+        if (m0 + BM <= M) store_swiglu(std::false_type{});
+        else store_swiglu(std::true_type{});
+    } else if (m0 + BM <= M) {
+        store_tile(std::false_type{});
+    } else {
+        store_tile(std::true_type{});
+    }
 }
 
 // One launch over the product's columns [n0, n0 + Nc) with BN-wide tiles.
 template <int BITS, int BN>
 static int launch_qgemm_cols(const GemmArgs &full, int n0, int Nc, hipStream_t stream) {
     GemmArgs a = full;
-    a.wq = full.wq + (size_t)n0 * ((size_t)full.K * BITS / 32);
-    a.s = full.s + (size_t)n0 * full.G;
-    a.b = full.b + (size_t)n0 * full.G;
-    a.bias = full.bias ? full.bias + n0 : nullptr;
-    a.y = full.y + n0;
+    if (full.swiglu_i) {
+        a.n_base = n0;
+    } else {
+        a.wq = full.wq + (size_t)n0 * ((size_t)full.K * BITS / 32);
+        a.s = full.s + (size_t)n0 * full.G;
+        a.b = full.b + (size_t)n0 * full.G;
+        a.bias = full.bias ? full.bias + n0 : nullptr;
+        a.y = full.y + n0;
+    }
     a.N = Nc;
     a.nt = (Nc + BN - 1) / BN;
     a.tiles = a.mt * a.nt;
@@ -350,17 +404,22 @@ static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream) {
     return launch_qgemm_cols<BITS, 256>(a, 0, N, stream);
 }
 
+// swiglu_half = I > 0: the weight stacks gate and up (N = 2I, I a multiple of 16) and y
+// receives act [M, I] = silu(gate) * up (row stride I).
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits,
-                      hipStream_t stream) {
+                      hipStream_t stream, int swiglu_half) {
     if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "qgemm: bits=%d", bits);
+    if (swiglu_half && (swiglu_half % 16 || N != 2 * swiglu_half)) return SC_EUNSUPPORTED;
     if (K % BK) return set_error(SC_EINVAL, "qgemm: K=%d not a multiple of %d", K, BK);
     if (((uintptr_t)x % 16) || ((uintptr_t)wq % 16))
         return set_error(SC_EINVAL, "qgemm: x and wq must be 16-byte aligned");
     GemmArgs a;
     a.x = x; a.wq = wq; a.s = s; a.b = b; a.bias = bias; a.y = y;
     a.M = M; a.N = N; a.K = K; a.G = K / BK;
-    a.ldy = N;
+    a.ldy = swiglu_half ? swiglu_half : N;
+    a.swiglu_i = swiglu_half;
+    a.n_base = 0;
     a.mt = (M + BM - 1) / BM;
     a.nt = a.tiles = 0;
     return bits == 4 ? launch_qgemm_t<4>(a, stream) : launch_qgemm_t<8>(a, stream);

@@ -65,7 +65,9 @@ def test_qmm_rmsnorm_matches_unfused(device, M, N, K, bits):
                                               (3, 1024, 1024, 8, True), (12, 512, 1024, 4, True),
                                               (1, 2048, 576, 4, True), (1, 256, 512, 4, True),
                                               (1, 64, 512, 8, False), (16, 1792, 4096, 4, True),
-                                              (32, 896, 2048, 8, False), (24, 1024, 3584, 4, False)])
+                                              (32, 896, 2048, 8, False), (24, 1024, 3584, 4, False),
+                                              (64, 1024, 1024, 4, False), (300, 1536, 2048, 8, True),
+                                              (600, 2048, 4096, 4, False)])
 def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     rng = np.random.default_rng(M * 7 + I + K)
     wq, s, b = _weights(rng, 2 * I, K, bits)
@@ -90,8 +92,9 @@ def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     # moves by a bf16 step of g or u (measured relative to the output's scale)
     a1, a2 = host_u16(act), host_u16(act2)
     assert max_abs_rel(a1, a2) <= 2e-3 and (bf16_ulp_diff(a1, a2) > 0).mean() < 0.02
-    if 8 < M <= 32:
-        # 9-32 rows: the product's own split-K pass applies the gate, on the same sums
+    if M > 8:
+        # 9-32 rows: the product's own split-K pass applies the gate, on the same sums;
+        # more rows: the GEMM pairs gate and up columns in its tiles, same k order
         assert torch.equal(act, act2)
     xin = host_u16(xn2)
     gu = quantized_matmul_f64(xin, wq, s, b, 64, bits)
@@ -101,11 +104,28 @@ def test_qmm_swiglu_matches_unfused(device, M, I, K, bits, norm):
     assert max_abs_rel(host_u16(act), ref) <= LINEAR_TOL
 
 
-@pytest.mark.parametrize("M,bits", [(9, 4), (16, 8), (32, 4)])
+@pytest.mark.parametrize("M,bits", [(2048, 4), (2048, 8)])
+def test_qmm_swiglu_prefill_shape_matches_unfused(device, M, bits):
+    # the Llama-3-8B gate|up at a 2048-token prefill: wide tiles plus the 128-wide
+    # launch for the partial last round, both pairing gate and up columns
+    rng = np.random.default_rng(M + bits)
+    I, K = 14336, 4096
+    wq, s, b = _weights(rng, 2 * I, K, bits)
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd = dev_bf16(_bf(rng, (M, K)))
+    print(f"qmm_swiglu M={M} I={I} K={K} W{bits}", flush=True)
+    act, _ = _lib.qmm_swiglu(xd, *W, bits=bits)
+    act2 = _lib.silu_mul(_lib.qmm(xd, *W, bits=bits))
+    torch.cuda.synchronize()
+    assert torch.equal(act, act2)
+
+
+@pytest.mark.parametrize("M,bits", [(9, 4), (16, 8), (32, 4), (200, 4), (1100, 8)])
 def test_qmm_swiglu_batch_with_bias(device, M, bits):
-    """9-32 rows: silu(gate) * up from the GEMV's split-K pass, with a linear bias
-    added to the rounded gate and up (as the plain product does), equals the plain
-    product followed by silu_mul bit for bit."""
+    """Batched rows: silu(gate) * up from the GEMV's split-K pass (9-32 rows) or the
+    GEMM's paired tiles (more), with a linear bias added to the rounded gate and up
+    (as the plain product does), equals the plain product followed by silu_mul bit
+    for bit."""
     rng = np.random.default_rng(M + 1000 * bits)
     I, K = 1536, 4096
     wq, s, b = _weights(rng, 2 * I, K, bits)
