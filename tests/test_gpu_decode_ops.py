@@ -165,6 +165,41 @@ def test_attention(device, B, S, H, Hkv, D, past, extra):
     assert err <= ATTN_TOL
 
 
+@pytest.mark.parametrize("growth", ["steep", "gentle"])
+def test_attention_prefill_running_max(device, growth):
+    # the 128-column kernel moves a column's running maximum only when it grew by more
+    # than 2^8 in probability: keys whose scores grow along the sequence make it move
+    # often ("steep": e^10 per 64-key block) or stay put with probabilities near 256
+    # ("gentle": 5.5 bits over the whole sequence); both must match the reference
+    B, S, H, Hkv, D = 1, 512, 32, 8, 128
+    rng = np.random.default_rng(17 if growth == "steep" else 18)
+    T_cap = S
+    q = rng.standard_normal((B * S, H * D)).astype(np.float32) * 0.5
+    k = rng.standard_normal((B, Hkv, T_cap, D)).astype(np.float32) * 0.5
+    # a shared direction in q and k whose weight grows with the key's position
+    dirv = rng.standard_normal(D).astype(np.float32)
+    dirv /= np.linalg.norm(dirv)
+    per_key = 10.0 / 64 if growth == "steep" else 5.5 * np.log(2) / S
+    scale = 1.0 / np.sqrt(D)
+    q += np.tile(dirv, H)[None, :] * 4.0
+    k += (np.arange(T_cap, dtype=np.float32)[:, None] * per_key / (4.0 * scale)) * dirv[None, :]
+    q, k = f32_to_bf16(q), f32_to_bf16(k)
+    v = _bf(rng, (B, Hkv, T_cap, D))
+    cnt = torch.tensor([0, 0], dtype=torch.int32, device="cuda")
+    out = _lib.attention(dev_bf16(q), B, S, H, Hkv, D, dev_bf16(k),
+                         dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2))), cnt, scale)
+    torch.cuda.synchronize()
+    rep = H // Hkv
+    q4 = bf16_to_f32(q).reshape(B, S, H, D).transpose(0, 2, 1, 3)
+    kk = np.repeat(bf16_to_f32(k), rep, axis=1)
+    vv = np.repeat(bf16_to_f32(v), rep, axis=1)
+    ref = attention_core(q4, kk, vv, scale, 0).transpose(0, 2, 1, 3).reshape(B * S, H * D)
+    got = bf16_to_f32(host_u16(out))
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    print(f"attention, running maximum {growth}: max-abs-rel {err:.2e}", flush=True)
+    assert np.isfinite(got).all() and err <= ATTN_TOL
+
+
 @pytest.mark.parametrize("B,S,H,Hkv,D,past,extra", [
     (1, 48, 32, 8, 128, 200, 40),     # 16-column workgroups
     (1, 300, 32, 8, 64, 17, 40),      # head_dim 64
