@@ -361,7 +361,25 @@ __global__ void __launch_bounds__(256) qgemv_finalize_kernel(const float *partia
     const int64_t total = (int64_t)M * N;
     auto value = [&](int64_t i) -> uint32_t {          // rounded product element i (+ bias)
         float v = 0.f;
-        for (int s = 0; s < splits; ++s) v += partials[(size_t)s * total + i];
+        // up to eight loads in flight (a loop of dependent adds issued one load at a
+        // time), summed in split order
+        int s = 0;
+        for (; s + 8 <= splits; s += 8) {
+            float p[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) p[u] = partials[(size_t)(s + u) * total + i];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v += p[u];
+        }
+        if (s + 4 <= splits) {
+            float p[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p[u] = partials[(size_t)(s + u) * total + i];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v += p[u];
+            s += 4;
+        }
+        for (; s < splits; ++s) v += partials[(size_t)s * total + i];
         uint32_t o = f2bf(v);
         if (bias) o = f2bf(bf2f(o) + bf2f(bias[i % N]));
         return o;
