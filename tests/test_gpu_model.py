@@ -114,7 +114,9 @@ def test_greedy_generation(device, weights, model, B, use_graphs):
     _, steps = OracleDecoder(SHAPE, weights).generate_greedy(ids, n, forced=new)
     agree = _margin_check(new, steps)
     print(f"greedy B={B} graphs={use_graphs}: argmax agreement {agree:.2f}", flush=True)
-    assert agree >= 0.8
+    # every token passed the margin check; exact argmax agreement measured 0.95-1.00
+    # (the misses are near-ties of the random-init logits)
+    assert agree >= 0.9
 
 
 def test_graph_matches_eager(device, model):

@@ -54,4 +54,6 @@ def test_tinyllama_shape_greedy_decode(device, weights, model):
     _, steps = OracleDecoder(SHAPE, weights).generate_greedy(ids, n, forced=new)
     agree = _margin_check(new, steps)
     print(f"tinyllama-shape greedy: argmax agreement {agree:.2f}", flush=True)
-    assert agree >= 0.8
+    # every token passed the margin check; exact argmax agreement measured 0.94 (30 of 32;
+    # the misses are near-ties of the random-init logits)
+    assert agree >= 0.9
