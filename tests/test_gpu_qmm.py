@@ -81,7 +81,9 @@ def test_golden_fixtures_both_kernels(device):
 @pytest.mark.parametrize("M", [1, 2, 4, 5, 8, 9, 16, 17, 31, 32])
 def test_gemv_random_shapes(device, bits, M):
     rng = np.random.default_rng(100 + M + bits)
-    for K, N in [(64, 1), (576, 33), (1024, 257), (4096, 96), (2048, 1000), (512, 71), (14336, 40)]:
+    # (6656, 48): 13 (W4) / 26 (W8) K splits at 9-32 rows, so the split-K pass sums
+    # blocks of eight and four partials and single ones
+    for K, N in [(64, 1), (576, 33), (1024, 257), (4096, 96), (2048, 1000), (512, 71), (14336, 40), (6656, 48)]:
         with_bias = (N % 2) == 1
         x, wq, s, b, bias = _case(rng, M, K, N, bits, with_bias)
         print(f"gemv M={M} K={K} N={N} bits={bits}", flush=True)
