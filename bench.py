@@ -87,6 +87,9 @@ def parse_args():
     p.add_argument("--attn-only", action="store_true",
                    help="run only the prefill attention of the Llama-3-8B heads at --prefill positions "
                         "(random q, k, v; for counter profiling)")
+    p.add_argument("--gemv16-only", action="store_true",
+                   help="run only the 9-32-row quantized GEMV on the batched-decode projection shapes "
+                        "(70B rank-0 shard at 32 rows, Llama-3-8B at 16; for counter profiling)")
     p.add_argument("--trunk-only", action="store_true",
                    help="prefill, then only eager whole-trunk decode launches (for counter profiling)")
     p.add_argument("--trunk-timeline", action="store_true",
@@ -558,6 +561,43 @@ def time_prefill_attention(cfg, B, P, reps):
         f"{flops / us / 1e6:.0f} TFLOP/s (causal half), {reps} launches")
 
 
+def time_batched_gemv(reps):
+    """W4 quantized products of the batched decode steps on random weights: per shape,
+    the average time of one call (the 9-32-row GEMV plus its split-K pass) over
+    `reps` back-to-back calls, and GB/s of its algorithmic bytes (packed weights,
+    scales and biases, x and y).  A 256 MiB copy runs first (counter scale)."""
+    import torch
+    from shardcompute_amd import _lib
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    shapes = [("70B-shard q|k|v", 32, 8192, 1280), ("70B-shard o", 32, 1024, 8192),
+              ("70B-shard gate|up", 32, 8192, 7168), ("70B-shard down", 32, 3584, 8192),
+              ("8B q|k|v", 16, 4096, 6144), ("8B o", 16, 4096, 4096),
+              ("8B gate|up", 16, 4096, 28672), ("8B down", 16, 14336, 4096)]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    for name, M, K, N in shapes:
+        wq, s, b = _lib.quantize(torch.randn((N, K), generator=g, device="cuda").mul_(0.02), bits=4)
+        x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        _lib.qmm(x, wq, s, b, bits=4, out=y)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            _lib.qmm(x, wq, s, b, bits=4, out=y)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        nbytes = N * K // 2 + N * (K // 64) * 4 + M * K * 2 + M * N * 2
+        log(f"gemv16-only: {name} M={M} K={K} N={N}: {us:.2f} us per call, {nbytes / us / 1e3:.0f} GB/s "
+            f"({nbytes / 1e6:.2f} MB), {reps} calls")
+        del wq, s, b, x, y
+
+
 def timed_prefill(model, ids, cache):
     """Seconds of the prefill forward of ``ids`` into ``cache`` (last position's
     logits), after one untimed prefill of the same shape into a scratch cache (the
@@ -677,6 +717,9 @@ def main():
     B, P, K, W = args.batch, args.prefill, args.steps, args.warmup
     if args.attn_only:
         time_prefill_attention(cfg, B, P, args.kernel_reps)
+        return
+    if args.gemv16_only:
+        time_batched_gemv(args.kernel_reps)
         return
     capacity = P + W + K + 8
     t_build = time.perf_counter()
