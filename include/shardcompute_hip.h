@@ -30,12 +30,13 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 10
+#define SC_ABI_VERSION 11
 
 /* Kernel selection for sc_qmm_bf16_path. */
-#define SC_QMM_PATH_AUTO 0 /* M <= 32: fused dequant-GEMV, else tiled MFMA GEMM */
+#define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV; 33-160: band kernel; above: GEMM     */
 #define SC_QMM_PATH_GEMV 1 /* fused dequant-GEMV (decode batches, M <= 32)      */
 #define SC_QMM_PATH_GEMM 2 /* LDS-staged dequant -> bf16 MFMA GEMM (prefill)     */
+#define SC_QMM_PATH_BAND 3 /* weight-streaming band kernel (M <= 256)            */
 
 /* ABI version of the loaded library (SC_ABI_VERSION at build time). */
 int sc_abi_version(void);
@@ -70,6 +71,16 @@ int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scal
                      const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
                      int group_size, int path, void *hip_stream);
 
+/*
+ * sc_qmm_bf16 on the band kernel (M <= 256, K a multiple of 512) with its plan
+ * pinned: waves per workgroup (4 or 8; 0 = automatic) and K splits (0 = automatic).
+ * For measurements of the plan; results do not depend on it beyond the split-K
+ * summation order.  Same reference call sites as sc_qmm_bf16.
+ */
+int sc_qmm_bf16_band(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                     const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                     int group_size, int waves, int ksplit, void *hip_stream);
+
 /* Size of the device array that sc_qmm_bf16_noalloc's split-K partials live in. */
 #define SC_QMM_NOALLOC_SCRATCH_BYTES (4u << 20)
 
@@ -79,10 +90,12 @@ int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scal
  * forbid allocation.  No counterpart in the reference (mx.quantized_matmul
  * allocates its output; this entry point allocates nothing at all).  Same
  * arguments, kernels and results as sc_qmm_bf16, bit for bit.  Where the 9-32-row
- * GEMV splits K across workgroups, its fp32 partials go to a file-scope device
- * array of SC_QMM_NOALLOC_SCRATCH_BYTES (one per GPU, held until the process
- * ends) instead of the library's growable buffer; a shape whose partials
- * (splits * M * N floats) exceed it returns -1 with a message.  The array's
+ * GEMV or the 33-160-row band kernel splits K across workgroups, its fp32 partials go
+ * to a file-scope device array of SC_QMM_NOALLOC_SCRATCH_BYTES (one per GPU, held
+ * until the process ends) instead of the library's growable buffer.  A shape whose
+ * partials (splits * M * N floats) exceed it runs on the next kernel that needs no
+ * scratch (the 32-column GEMV or the GEMM): within the same 1e-2 of the exact product
+ * but not bit for bit equal to sc_qmm_bf16.  The array's
  * address is looked up on the first call on each device (no allocation, no
  * synchronisation).  Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (concurrent streams) race.  Each launch writes every
@@ -184,10 +197,13 @@ int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
  * xn = RMSNorm(x + residual) when norm_weight_or_null is given (xn_out and, with a
  * residual, h_out receive xn and x + residual as for sc_qmm_rmsnorm_bf16).  The
  * decode GEMV (M <= 8) pairs gate row i with up row I + i inside one tile and writes
- * act [M, I] directly; at 9-32 rows the split-K finalize rounds gate and up to bf16
- * (bias after rounding) and writes act [M, I]; otherwise the product goes to
- * gate_up_scratch [M, 2I] and the standalone sc_silu_mul_bf16 follows (the same
- * values).  Outputs must not overlap the inputs.
+ * act [M, I] directly; at 9-32 rows (split-K GEMV) and 33-160 rows (band kernel, K a
+ * multiple of 512) the split-K pass rounds gate and up to bf16 (bias after rounding)
+ * and writes act [M, I]; above that the GEMM pairs gate and up columns in its tiles
+ * and writes act itself (I a multiple of 16).  gate_up_scratch [M, 2I] is required but
+ * used only where none of these applies: then the product goes there and the
+ * standalone sc_silu_mul_bf16 follows (the same values).  Outputs must not overlap
+ * the inputs.
  * Replaces ParallelMLP.forward's gate/up projections and activation
  * (src/shardcompute/parallel/mlp.py:241-245), after the post-attention layernorm
  * (transformer.py:249-250).
@@ -386,9 +402,11 @@ void sc_decode_plan_destroy(void *plan);
  * then 6 per layer: q|k|v, attention, key-range merge, o, gate|up, down), the
  * 100 MHz real-time clock at four points: the op's items all computed (k = 0), its
  * output published (1), its input polled (2) and staged (3), at
- * stamps[(w * ops + j) * 4 + k]; (plan, 0) frees it.  sc_decode_plan_read_trace
- * copies the last launch's stamps (n entries at least workgroups * ops * 4;
- * stamps may be null to query the sizes), synchronously.
+ * stamps[(w * ops + j) * 4 + k]; (plan, 0) stops recording for later launches.  The
+ * buffer stays allocated until sc_decode_plan_destroy, so a graph captured while
+ * tracing was on may still be replayed.  sc_decode_plan_read_trace copies the stamps
+ * of the last launch that recorded (n entries at least workgroups * ops * 4; stamps
+ * may be null to query the sizes), synchronously.
  */
 int sc_decode_plan_trace(void *plan, int enable);
 int sc_decode_plan_read_trace(void *plan, uint32_t *stamps, int64_t n, int *workgroups, int *ops);

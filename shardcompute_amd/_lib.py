@@ -14,8 +14,8 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 10
-PATH_AUTO, PATH_GEMV, PATH_GEMM = 0, 1, 2
+ABI_VERSION = 11
+PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_BAND = 0, 1, 2, 3
 
 # Exported symbols (must match include/shardcompute_hip.h).
 EXPORTS = (
@@ -24,6 +24,7 @@ EXPORTS = (
     "sc_qmm_bf16",
     "sc_qmm_bf16_path",
     "sc_qmm_bf16_noalloc",
+    "sc_qmm_bf16_band",
     "sc_vocab_gather_bf16",
     "sc_qembed_gather_bf16",
     "sc_dequantize_bf16",
@@ -82,6 +83,8 @@ def load():
         lib.sc_qmm_bf16_path.restype = i32
         lib.sc_qmm_bf16_noalloc.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
         lib.sc_qmm_bf16_noalloc.restype = i32
+        lib.sc_qmm_bf16_band.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, i32, i32, p]
+        lib.sc_qmm_bf16_band.restype = i32
         lib.sc_vocab_gather_bf16.argtypes = [p, i32, i64, p, i64, i64, i64, p, p]
         lib.sc_vocab_gather_bf16.restype = i32
         lib.sc_qembed_gather_bf16.argtypes = [p, i32, i64, p, p, p, i64, i64, i64, i32, i32, p, p]
@@ -175,11 +178,14 @@ def _bf16(t, name):
     return t
 
 
-def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO, out=None, no_alloc=False):
+def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO, out=None, no_alloc=False,
+        band_plan=None):
     """y = bf16(x @ dequant(wq, scales, biases)^T) (+ bias), x [..., K] -> [..., N].
 
     ``no_alloc``: call ``sc_qmm_bf16_noalloc`` (the library allocates nothing;
-    pass ``out`` too for a call that allocates nothing at all)."""
+    pass ``out`` too for a call that allocates nothing at all).
+    ``band_plan``: (waves, ksplit) pins the band kernel's plan (``sc_qmm_bf16_band``;
+    0 = automatic), for measurements."""
     lib = load()
     _require_gpu(x, wq, scales, biases, bias)
     _bf16(x, "x"), _bf16(scales, "scales"), _bf16(biases, "biases")
@@ -209,7 +215,12 @@ def qmm(x, wq, scales, biases, bias=None, bits=4, group_size=64, path=PATH_AUTO,
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         ev0.record()
-    if no_alloc:
+    if band_plan is not None:
+        if no_alloc or path not in (PATH_AUTO, PATH_BAND):
+            raise ValueError("band_plan selects the band kernel (path AUTO or BAND, not no_alloc)")
+        rc = lib.sc_qmm_bf16_band(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),
+                                  M, N, K, bits, group_size, int(band_plan[0]), int(band_plan[1]), st)
+    elif no_alloc:
         if path != PATH_AUTO:
             raise ValueError("the allocation-free entry point chooses its kernel itself (path must be AUTO)")
         rc = lib.sc_qmm_bf16_noalloc(_ptr(x2), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(y),

@@ -23,6 +23,9 @@ int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
                       int swiglu_half = 0);
+int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
+                      const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
+                      bool no_alloc, int swiglu_half, int force_nw, int force_split);
 int launch_vocab_gather(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
                         int64_t D, int64_t vocab_start, uint16_t *out, hipStream_t stream);
 int launch_qembed_gather(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq, const uint16_t *s,
@@ -159,7 +162,16 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
     int rc = check_qmm(x, wq, s, b, y, M, N, K, bits, group_size);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (path == SC_QMM_PATH_AUTO) path = (M <= 32) ? SC_QMM_PATH_GEMV : SC_QMM_PATH_GEMM;
+    // 33-160 rows: the band kernel (measured faster than the GEMM's 256-row tiles up to
+    // 128 rows, slower at 256)
+    if (path == SC_QMM_PATH_AUTO) path = M <= 32 ? SC_QMM_PATH_GEMV : M <= 160 ? SC_QMM_PATH_BAND : SC_QMM_PATH_GEMM;
+    if (path == SC_QMM_PATH_BAND) {
+        // 33-256 rows (or any M <= 256 when asked for): the weight-streaming band kernel;
+        // shapes it does not take (K not a multiple of 512) go to the GEMM
+        rc = launch_qgemm_band(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, 0, 0);
+        if (rc != SC_EUNSUPPORTED) return rc;
+        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+    }
     if (path == SC_QMM_PATH_GEMV) {
         // M <= 8: persistent LDS-DMA GEMV; otherwise (or when x does not fit its
         // LDS) the 16-column split-K GEMV; K not a multiple of 512 (W4) / 256 (W8)
@@ -248,6 +260,12 @@ static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw,
         rc = launch_qgemv16(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half);
         if (rc != SC_EUNSUPPORTED) return rc;
     }
+    if (M > 32 && M <= 160) {
+        // the band kernel's split-K pass applies silu(gate) * up itself
+        rc = launch_qgemm_band(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half, 0,
+                               0);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
     if (M > 32) {
         // the GEMM pairs gate and up columns in its tiles and writes act itself
         rc = launch_qgemm_mfma(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, (int)swiglu_half);
@@ -279,6 +297,21 @@ int sc_qmm_bf16_path(const uint16_t *x, const uint32_t *wq, const uint16_t *scal
                      const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
                      int group_size, int path, void *hip_stream) {
     return qmm_dispatch(x, wq, scales, biases, bias_or_null, y, M, N, K, bits, group_size, hip_stream, path);
+}
+
+int sc_qmm_bf16_band(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                     const uint16_t *bias_or_null, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
+                     int group_size, int waves, int ksplit, void *hip_stream) {
+    int rc = check_qmm(x, wq, scales, biases, y, M, N, K, bits, group_size);
+    if (rc) return rc;
+    if (waves != 0 && waves != 4 && waves != 8) return set_error(SC_EINVAL, "qmm_band: waves=%d (0, 4 or 8)", waves);
+    if (ksplit < 0 || ksplit > 65535) return set_error(SC_EINVAL, "qmm_band: ksplit=%d", ksplit);
+    rc = launch_qgemm_band(x, wq, scales, biases, bias_or_null, y, (int)M, (int)N, (int)K, bits,
+                           reinterpret_cast<hipStream_t>(hip_stream), false, 0, waves, ksplit);
+    if (rc == SC_EUNSUPPORTED)
+        return set_error(SC_EUNSUPPORTED, "qmm_band: M=%lld K=%lld not taken (M <= 256, K %% 512 == 0, 16-byte "
+                         "aligned scales and biases)", (long long)M, (long long)K);
+    return rc;
 }
 
 int sc_qmm_bf16_noalloc(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,

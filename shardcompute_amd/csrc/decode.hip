@@ -12,6 +12,7 @@
 #include "sc_common.h"
 
 #include <math.h>
+#include <float.h>
 
 namespace sc {
 
@@ -239,11 +240,20 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
         sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * scale_log2 : -INFINITY;
     }
     if (MASKED) {
+        // The scores are in log2 units, so the mask is scaled by log2(e).  A finite mask
+        // value stays finite: one below -FLT_MAX / log2(e) (finfo(float32).min, the
+        // usual padding value) is clamped to -FLT_MAX instead of overflowing to -inf.
+        // The reference adds it unscaled in fp32 and gets a finite score, so a row whose
+        // visible keys all carry it gets uniform weights there, and must not become 0/0
+        // here.  -inf stays -inf.
         constexpr float LOG2E = 1.4426950408889634f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
             const int key = kb + 16 * (r >> 2) + 4 * g + (r & 3);
-            if (key <= limit) sv[r] += mrow[(long)key * mst] * LOG2E;
+            if (key <= limit) {
+                const float mv = mrow[(long)key * mst];
+                sv[r] += (mv == -INFINITY) ? -INFINITY : fmaxf(mv * LOG2E, -FLT_MAX);
+            }
         }
     }
     float bm = sv[0];

@@ -1309,16 +1309,15 @@ int decode_plan_status(void *plan, unsigned *status) {
 int decode_plan_trace(void *plan, int enable) {
     DecodePlan *pl = static_cast<DecodePlan *>(plan);
     if (!pl) return set_error(SC_EINVAL, "decode_plan_trace: null plan");
+    // The stamp buffer, once allocated, lives until sc_decode_plan_destroy: a graph
+    // captured while tracing was on keeps writing stamps into it on every replay, also
+    // after tracing is switched off for later launches.
     const size_t bytes = (size_t)pl->P * pl->args.nops * 4 * sizeof(uint32_t);
     if (enable && !pl->d_trace) {
         SC_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&pl->d_trace), bytes));
         SC_HIP_CHECK(hipMemset(pl->d_trace, 0, bytes));
-    } else if (!enable && pl->d_trace) {
-        SC_HIP_CHECK(hipDeviceSynchronize());
-        SC_HIP_CHECK(hipFree(pl->d_trace));
-        pl->d_trace = nullptr;
     }
-    pl->args.trace = pl->d_trace;
+    pl->args.trace = enable ? pl->d_trace : nullptr;
     return SC_OK;
 }
 
@@ -1328,7 +1327,7 @@ int decode_plan_read_trace(void *plan, uint32_t *host, int64_t n, int *P, int *n
     *P = pl->P;
     *nops = pl->args.nops;
     if (!host) return SC_OK;
-    if (!pl->d_trace) return set_error(SC_EINVAL, "decode_plan_read_trace: tracing is not enabled");
+    if (!pl->d_trace) return set_error(SC_EINVAL, "decode_plan_read_trace: tracing was never enabled");
     const int64_t need = (int64_t)pl->P * pl->args.nops * 4;
     if (n < need) return set_error(SC_EINVAL, "decode_plan_read_trace: %lld entries needed", (long long)need);
     SC_HIP_CHECK(hipMemcpy(host, pl->d_trace, (size_t)need * sizeof(uint32_t), hipMemcpyDeviceToHost));

@@ -410,7 +410,7 @@ static constexpr int kScratchDevices = 64;
 static float *g_scratch_ptr[kScratchDevices];
 static std::mutex g_scratch_mu;
 
-static int noalloc_scratch(float **out) {
+int qmm_noalloc_scratch(float **out) {
     int dev = 0;
     SC_HIP_CHECK(hipGetDevice(&dev));
     if (dev < 0 || dev >= kScratchDevices) return set_error(SC_EINVAL, "device id %d out of range", dev);
@@ -502,11 +502,12 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
         const size_t need = (size_t)p.splits * M * N;
         if (no_alloc) {
             constexpr size_t cap = SC_QMM_NOALLOC_SCRATCH_BYTES / sizeof(float);
+            // above the array: the caller moves on to a kernel that needs no scratch
             if (need > cap)
-                return set_error(SC_EINVAL, "qmm_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K scratch, above "
-                                            "the %zu-byte maximum", M, N, K, need * sizeof(float),
+                return set_error(SC_EUNSUPPORTED, "qmm_noalloc: M=%d N=%d K=%d needs %zu bytes of split-K scratch, "
+                                                  "above the %zu-byte maximum", M, N, K, need * sizeof(float),
                                  (size_t)SC_QMM_NOALLOC_SCRATCH_BYTES);
-            const int rc = noalloc_scratch(&a.partials);
+            const int rc = qmm_noalloc_scratch(&a.partials);
             if (rc) return rc;
         } else {
             SplitKScratch ws;
@@ -522,14 +523,18 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     return set_error(SC_EUNSUPPORTED, "qgemv16: bits=%d", bits);
 #undef SC_G16
     if (rc) return rc;
-    if (with_partials) {
-        const int64_t total = (int64_t)M * (swiglu_half ? swiglu_half : N);
-        int64_t blocks = (total + 255) / 256;
-        if (blocks > 4096) blocks = 4096;
-        hipLaunchKernelGGL(qgemv_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, a.partials, p.splits,
-                           M, N, bias, y, swiglu_half);
-        SC_HIP_CHECK(hipGetLastError());
-    }
+    if (with_partials) return launch_qmm_finalize(a.partials, p.splits, M, N, bias, y, swiglu_half, stream);
+    return SC_OK;
+}
+
+int launch_qmm_finalize(const float *partials, int splits, int M, int N, const uint16_t *bias, uint16_t *y, int half,
+                        hipStream_t stream) {
+    const int64_t total = (int64_t)M * (half ? half : N);
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(qgemv_finalize_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, partials, splits, M, N,
+                       bias, y, half);
+    SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
 }
 

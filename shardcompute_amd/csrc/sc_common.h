@@ -247,6 +247,16 @@ struct SplitKScratch {
 };
 int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out);
 
+// The allocation-free entry point's split-K partials: this device's file-scope
+// array of SC_QMM_NOALLOC_SCRATCH_BYTES (address looked up once per device).
+int qmm_noalloc_scratch(float **out);
+
+// y = bf16(sum over splits of partials [splits, M, N] in split order) (+ bias after
+// rounding); with half > 0 the product is gate|up stacked (N = 2 half) and y [M, half]
+// receives silu(gate) * up of the rounded values.
+int launch_qmm_finalize(const float *partials, int splits, int M, int N, const uint16_t *bias, uint16_t *y, int half,
+                        hipStream_t stream);
+
 // Arg-max key of a bf16 value: the order-preserving 16-bit image of the value
 // (NaN above +inf, -0.0 equal to +0.0) over ~index, so the larger key is the larger
 // value and, among equal values, the smaller index.  No key is 0.

@@ -170,8 +170,9 @@ class TrunkPlan:
     OP_KINDS = ("qkv", "attn", "merge", "o", "gate_up", "down")
 
     def trace(self, enable: bool = True):
-        """Make later launches record the per-op timeline (allocates a stamp buffer;
-        not under graph capture).  ``trace(False)`` frees it."""
+        """Make later launches record the per-op timeline (allocates a stamp buffer
+        once; not under graph capture).  ``trace(False)`` stops recording; the buffer
+        lives until the plan is closed, so graphs captured while tracing stay valid."""
         lib = _lib.load()
         _lib._check(lib.sc_decode_plan_trace(self._handle, 1 if enable else 0), "sc_decode_plan_trace")
 

@@ -228,6 +228,17 @@ def _mask_for(rng, kind, B, H, S, T):
         return m
     if kind == "rowcol":                    # [S, T]: leading dimensions broadcast
         return (rng.standard_normal((S, T)) * 1.5).astype(np.float32)
+    if kind == "padmin":                    # [B, 1, S, T]: left padding with finfo(float32).min
+        # sequence b's first pad[b] keys are padding; its padded query rows (prefill from
+        # position 0) see only padding keys, so every visible key of such a row carries
+        # finfo.min: the reference's softmax gives them uniform weights (finite rows)
+        m = np.zeros((B, 1, S, T), np.float32)
+        for b in range(B):
+            pad = 3 + 7 * b
+            m[b, 0, :, :pad] = np.finfo(np.float32).min
+        return m
+    if kind == "allmin":                    # [B, 1, S, T]: every key finfo(float32).min
+        return np.full((B, 1, S, T), np.finfo(np.float32).min, np.float32)
     raise ValueError(kind)
 
 
@@ -237,6 +248,9 @@ def _mask_for(rng, kind, B, H, S, T):
     (1, 1, 32, 8, 128, 2047, 256, "pad"),   # one position, keys split over workgroups
     (3, 1, 8, 1, 128, 300, 0, "full"),      # one position, 8 heads per KV head
     (1, 200, 32, 8, 128, 0, 40, "rowcol"),
+    (2, 64, 32, 8, 128, 0, 0, "padmin"),    # rows masked everywhere with finfo.min: uniform
+    (1, 1, 32, 8, 128, 300, 0, "allmin"),   # one position, every key finfo.min, split ranges
+    (2, 40, 8, 2, 64, 20, 8, "allmin"),     # after a cache: the causal limit still applies
 ])
 def test_attention_additive_mask(device, B, S, H, Hkv, D, past, extra, kind):
     rng = np.random.default_rng(B + S + past)
