@@ -28,8 +28,9 @@ Printed (one JSON line on stdout):
   per launch, averaged over the 129 launches of one decode step, over the average
   launch duration (HIP events on the replay stream around graph replays of exactly
   those launches, so the average is the kernels' own), against 8 TB/s;
-* ``cpu_baseline``: the C restatement of the quantized matmul (OpenMP, fp64
-  accumulation) timed on this host on a bounded sample: decoder layer 0's four
+* ``cpu_baseline``: a CPU restatement of the quantized matmul, not MLX (MLX's CPU
+  backend is not available; ``oracle/qmm_fast.c``: fp32 accumulation, AVX2 + FMA,
+  OpenMP over this host's cores) timed on a bounded sample: decoder layer 0's four
   projections plus 1/32 of the lm_head rows at M = batch, repeated for ~10 s,
   scaled to tokens/s of the 32-layer model's linear layers;
 * ``prefill.qgemm_roofline``: the prefill quantized GEMM at M = prompt tokens on
@@ -39,8 +40,11 @@ Printed (one JSON line on stdout):
   of the 128256 x 4096 table (GB/s on ids + written rows + unique in-shard rows
   read) and that configuration's W4 lm_head at M = 64; batch-16 decode of the
   headline model; the batch-1 decode qGEMV at 8 bits; TinyLlama-shape W4
-  decode (32-token prompt, batch 1); and the Llama-3-70B rank-0-of-8 shard at
-  batch 32 after a 1024-token prefill, W4 and W8 (all-reduces as identity).
+  decode (32-token prompt, batch 1); the Llama-3-70B rank-0-of-8 shard at
+  batch 32 after a 1024-token prefill, W4 and W8 (all-reduces as identity); and
+  the standalone quantized-linear sweep (the six TinyLlama / Llama-3-8B
+  projection shapes x M in {1, 8, 32, 512, 2048} x W4/W8, GPU time, GB/s or
+  TFLOP/s and roofline fraction, beside the CPU restatement's time).
 """
 import argparse
 import asyncio
@@ -75,7 +79,10 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=16, help="untimed decode steps")
     p.add_argument("--batch", type=int, default=1)
     p.add_argument("--prefill", type=int, default=2048)
-    p.add_argument("--layers", type=int, default=LLAMA3_8B["layers"])
+    p.add_argument("--layers", type=int, default=None, help="decoder layers (default: the model's)")
+    p.add_argument("--model", choices=("llama3-8b", "tinyllama"), default="llama3-8b",
+                   help="decoder shape of the headline run (the JSON line is the Llama-3-8B one; tinyllama is "
+                        "for the timeline and kernel-only diagnostics)")
     p.add_argument("--bits", type=int, default=4, choices=(4, 8))
     p.add_argument("--kernel-reps", type=int, default=5, help="graph replays of the per-launch GEMV timing")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -87,6 +94,8 @@ def parse_args():
     p.add_argument("--attn-only", action="store_true",
                    help="run only the prefill attention of the Llama-3-8B heads at --prefill positions "
                         "(random q, k, v; for counter profiling)")
+    p.add_argument("--sweep-only", action="store_true",
+                   help="only the standalone quantized-linear sweep (every (K, N), M, W4/W8), JSON on stdout")
     p.add_argument("--gemv16-only", action="store_true",
                    help="run only the 9-32-row quantized GEMV on the batched-decode projection shapes "
                         "(70B rank-0 shard at 32 rows, Llama-3-8B at 16; for counter profiling)")
@@ -413,14 +422,16 @@ def cpu_baseline(model, batch, bits, seconds):
     rng = np.random.default_rng(0)
     xs = {k: (rng.standard_normal((batch, k)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
           for k in {s[3] for s in sample}}
+    for wq, s, b, k in sample:                   # warm (thread pool, pages)
+        cref.qmm_fast_bf16(xs[k], wq, s, b, bits=bits, threads=threads)
     reps, t_layer, t_lm = 0, 0.0, 0.0
     t_start = time.perf_counter()
     while reps == 0 or (time.perf_counter() - t_start) < seconds:
         t0 = time.perf_counter()
         for wq, s, b, k in sample:
-            cref.qmm_bf16(xs[k], wq, s, b, bits=bits, threads=threads)
+            cref.qmm_fast_bf16(xs[k], wq, s, b, bits=bits, threads=threads)
         t1 = time.perf_counter()
-        cref.qmm_bf16(xs[lm[3]], lm[0], lm[1], lm[2], bits=bits, threads=threads)
+        cref.qmm_fast_bf16(xs[lm[3]], lm[0], lm[1], lm[2], bits=bits, threads=threads)
         t2 = time.perf_counter()
         t_layer += t1 - t0
         t_lm += t2 - t1
@@ -431,7 +442,8 @@ def cpu_baseline(model, batch, bits, seconds):
             "host_cores": host["affinity_cores"], "cpu_model": host["model"],
             "threads_note": (f"OpenMP threads = min(affinity cores, 16): {threads} of the "
                              f"{host['affinity_cores']} cores this process may run on"),
-            "sample": (f"oracle C restatement (fp64 accumulate, OpenMP) of the W{bits} g64 quantized matmuls: "
+            "sample": (f"CPU restatement, not MLX (oracle/qmm_fast.c: fp32 accumulation, AVX2 + FMA, OpenMP) of "
+                       f"the W{bits} g64 quantized matmuls: "
                        f"decoder layer 0's q|k|v, o, gate|up, down plus lm_head rows [0, {rows}) at M={batch}, "
                        f"{reps} repetitions in {time.perf_counter() - t_start:.1f} s, scaled x{model.num_layers} "
                        f"layers and x32 lm_head rows; attention and norms not included")}
@@ -516,6 +528,98 @@ def bench_lm_head_m64(reps=10):
     del wq, s, b, x, y
     return {"M": M, "N": N, "K": K, "bits": 4, "bytes": int(nbytes), "avg_us": round(us, 2), "GBs": round(gbs, 1),
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 1)}
+
+
+SWEEP_KN = [(2048, 2560), (2048, 5632), (5632, 2048), (4096, 6144), (4096, 14336), (14336, 4096)]
+SWEEP_M = [1, 8, 32, 512, 2048]
+
+
+def bench_qmm_sweep(reps=5):
+    """The standalone quantized-linear sweep: x bf16 N(0,1) [M, K], W [N, K] N(0, 0.02)
+    quantized W4 and W8 g64, every (K, N) of the TinyLlama and Llama-3-8B projections at
+    M in {1, 8, 32, 512, 2048}, through sc_qmm_bf16 (the kernel it selects).
+
+    GPU: enough copies of the packed weights to exceed the 256 MB last-level cache
+    (at least 512 MB in all), one product per copy captured in a HIP graph, HIP events
+    around ``reps`` replays; GB/s on the algorithmic bytes (M <= 32) or TFLOP/s
+    (M >= 512) against 8 TB/s and 2.5 PFLOP/s.  CPU: the vectorised C restatement
+    (fp32 accumulation, AVX2 + FMA, OpenMP on this host's cores; not MLX) on a sample
+    of the same product (min(M, 64) rows of x, min(N, 256) weight rows), scaled
+    linearly to the full M x N."""
+    import numpy as np
+    import torch
+    from oracle import cref
+    from shardcompute_amd import _lib
+    if not cref.available():
+        cref.build()
+    threads = cref.default_threads()
+    host = host_cpu()
+    rows = []
+    g = torch.Generator(device="cuda")
+    g.manual_seed(8)
+    for bits in (4, 8):
+        for K, N in SWEEP_KN:
+            wq, sc, bi = _lib.quantize(torch.randn((N, K), generator=g, device="cuda").mul_(0.02), bits=bits)
+            wbytes = N * K * bits // 8 + N * (K // 64) * 4
+            copies = max(1, min(200, -(-(512 << 20) // wbytes)))
+            ws = [(wq, sc, bi)] + [(wq.clone(), sc.clone(), bi.clone()) for _ in range(copies - 1)]
+            wq_h = wq[:256].cpu().view(torch.int32).numpy().view(np.uint32)
+            s_h = sc[:256].cpu().view(torch.int16).numpy().view(np.uint16)
+            b_h = bi[:256].cpu().view(torch.int16).numpy().view(np.uint16)
+            for M in SWEEP_M:
+                x = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
+                y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+                for w in ws[:2]:
+                    _lib.qmm(x, *w, bits=bits, out=y)          # warm: plans and scratch outside capture
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for w in ws:
+                        _lib.qmm(x, *w, bits=bits, out=y)
+                gr.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    gr.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+                nbytes = qmm_bytes(M, N, K, bits)
+                flops = 2.0 * M * N * K
+                kernel = ("gemv" if M <= 32 else "band" if M <= 160 and K % 512 == 0 else "gemm")
+                row = {"bits": bits, "M": M, "K": K, "N": N, "kernel": kernel, "gpu_us": round(us, 2)}
+                if M <= 32:
+                    gbs = nbytes / (us * 1e-6) / 1e9
+                    row.update(bound="hbm", GBs=round(gbs, 1), frac=round(gbs / HBM_PEAK_GBS, 4))
+                else:
+                    tf = flops / (us * 1e-6) / 1e12
+                    row.update(bound="mfma", TFLOPs=round(tf, 1), frac=round(tf * 1e12 / MFMA_BF16_PEAK, 4))
+                # CPU restatement on a sample, scaled to the full product
+                Ms, Ns = min(M, 64), min(N, 256)
+                x_h = x[:Ms].cpu().view(torch.int16).numpy().view(np.uint16)
+                cref.qmm_fast_bf16(x_h, wq_h[:Ns], s_h[:Ns], b_h[:Ns], bits=bits, threads=threads)
+                t0 = time.perf_counter()
+                n_cpu = 0
+                while n_cpu == 0 or time.perf_counter() - t0 < 0.05:
+                    cref.qmm_fast_bf16(x_h, wq_h[:Ns], s_h[:Ns], b_h[:Ns], bits=bits, threads=threads)
+                    n_cpu += 1
+                cpu_us = (time.perf_counter() - t0) / n_cpu * 1e6 * (M / Ms) * (N / Ns)
+                row.update(cpu_us_est=round(cpu_us, 1), gpu_vs_cpu=round(cpu_us / us, 1))
+                rows.append(row)
+                del x, y, gr
+            del ws, wq, sc, bi
+            torch.cuda.empty_cache()
+    for r in rows:
+        perf = f"{r['GBs']:.0f} GB/s" if r["bound"] == "hbm" else f"{r['TFLOPs']:.0f} TFLOP/s"
+        log(f"sweep W{r['bits']} M={r['M']:4d} K={r['K']:5d} N={r['N']:5d} {r['kernel']:4s}: {r['gpu_us']:8.2f} us "
+            f"{perf:>14s} ({100 * r['frac']:.1f} %), CPU {r['cpu_us_est'] / 1e3:.2f} ms (x{r['gpu_vs_cpu']})")
+    return {"rows": rows,
+            "cpu": {"kind": "CPU restatement, not MLX: oracle/qmm_fast.c (fp32 accumulation, AVX2 + FMA, OpenMP)",
+                    "threads": threads, "host_cores": host["affinity_cores"], "cpu_model": host["model"],
+                    "sample": "min(M, 64) rows of x and min(N, 256) weight rows, repeated for >= 50 ms, "
+                              "scaled linearly by (M / rows) x (N / weight rows)"},
+            "gpu": "graph replays over >= 512 MB of weight copies; GB/s at M <= 32, TFLOP/s at M >= 512"}
 
 
 def bench_w8_gemv(reps):
@@ -677,6 +781,7 @@ def run_extras(model, args):
         ("vocab_gather_config3", lambda: bench_vocab_gather()),
         ("lm_head_m64_config3", lambda: bench_lm_head_m64()),
         ("batch16_llama3_8b_w4", lambda: bench_batch16(model, 32)),
+        ("qmm_sweep_config2", lambda: bench_qmm_sweep()),
     ]
     if args.extras_models:
         jobs += [
@@ -713,13 +818,18 @@ def main():
         log("no GPU visible")
         sys.exit(1)
     _lib.load()
-    cfg = dict(LLAMA3_8B)
+    cfg = dict(LLAMA3_8B if args.model == "llama3-8b" else TINYLLAMA)
+    if args.layers is None:
+        args.layers = cfg["layers"]
     B, P, K, W = args.batch, args.prefill, args.steps, args.warmup
     if args.attn_only:
         time_prefill_attention(cfg, B, P, args.kernel_reps)
         return
     if args.gemv16_only:
         time_batched_gemv(args.kernel_reps)
+        return
+    if args.sweep_only:
+        print(json.dumps(bench_qmm_sweep()), flush=True)
         return
     capacity = P + W + K + 8
     t_build = time.perf_counter()
@@ -766,7 +876,8 @@ def main():
         t_us = time_trunk_launches(dec, args.kernel_reps)
         tl = plan.timeline()
         plan.trace(False)
-        tl.update({"workload": f"Llama-3-8B-shape W{args.bits}g64 whole-trunk decode launch, batch 1, context "
+        shape = "Llama-3-8B" if args.model == "llama3-8b" else "TinyLlama-1.1B"
+        tl.update({"workload": f"{shape}-shape W{args.bits}g64 whole-trunk decode launch, batch 1, context "
                                f"{cache.length}", "layers": args.layers, "avg_launch_us": round(t_us, 1),
                    "stamps": "s_memrealtime (100 MHz) by each workgroup's control wave, last of "
                              f"{args.kernel_reps + 1} back-to-back launches"})

@@ -356,8 +356,9 @@ int sc_add_i32(int32_t *counters, int64_t n, int32_t delta, void *hip_stream);
  * `ids[0]` its token id.  After the launch `h_out` holds the residual stream that
  * the final RMSNorm + lm_head read, and every layer's cache holds the new position.
  *
- * sc_decode_plan_create validates the shapes (head_dim 128, at most 4 query heads per
- * kv head, widths multiples of 512 up to 16384, group size 64, the attention rows and
+ * sc_decode_plan_create validates the shapes (head_dim 128 with at most 4 query heads
+ * per kv head, or head_dim 64 with at most 8; widths multiples of 512 up to 16384,
+ * group size 64, the attention rows and
  * key ranges splitting over the device's CUs, the whole working set within one CU's
  * LDS), uploads the per-layer pointer table and allocates the plan's exchange buffers
  * (a few MB; -2 for a shape it does not take); sc_decode_plan_run enqueues the

@@ -1,4 +1,5 @@
-"""ctypes binding of ``qmm_ref.c`` (the C restatement) — TEST INFRASTRUCTURE ONLY.
+"""ctypes binding of ``qmm_ref.c`` (the C restatement) and ``qmm_fast.c`` (the
+vectorised CPU restatement timed as the CPU baseline) — TEST INFRASTRUCTURE ONLY.
 
 ``build()`` compiles it with gcc through ``oracle/Makefile``; ``load()`` opens the
 built library.  Used by the tests as a second, independent implementation of
@@ -32,6 +33,8 @@ def load():
         p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         lib.oref_qmm_bf16.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, i32]
         lib.oref_qmm_bf16.restype = i32
+        lib.oref_qmm_fast_bf16.argtypes = [p, p, p, p, p, p, i64, i64, i64, i32, i32, i32]
+        lib.oref_qmm_fast_bf16.restype = i32
         lib.oref_vocab_gather_bf16.argtypes = [p, i32, i64, p, i64, i64, i64, p, i32]
         lib.oref_vocab_gather_bf16.restype = i32
         _lib = lib
@@ -68,6 +71,27 @@ def qmm_bf16(x, wq, scales, biases, bias=None, group_size=64, bits=4, threads=No
                            group_size, threads or default_threads())
     if rc != 0:
         raise ValueError(f"oref_qmm_bf16 failed with {rc}")
+    return y
+
+
+def qmm_fast_bf16(x, wq, scales, biases, bias=None, group_size=64, bits=4, threads=None):
+    """The vectorised fp32 CPU restatement (qmm_fast.c): the timed CPU baseline."""
+    lib = load()
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    b = np.ascontiguousarray(biases, dtype=np.uint16)
+    M, K = x.shape
+    N = wq.shape[0]
+    y = np.empty((M, N), dtype=np.uint16)
+    bptr = None
+    if bias is not None:
+        bias = np.ascontiguousarray(bias, dtype=np.uint16)
+        bptr = _ptr(bias)
+    rc = lib.oref_qmm_fast_bf16(_ptr(x), _ptr(wq), _ptr(s), _ptr(b), bptr, _ptr(y), M, N, K, bits,
+                                group_size, threads or default_threads())
+    if rc != 0:
+        raise ValueError(f"oref_qmm_fast_bf16 failed with {rc}")
     return y
 
 

@@ -59,8 +59,9 @@ constexpr int SLOT = 4096 + 512;            // item bytes + 16 rows x 8 groups o
 #endif
 constexpr int TRING = SC_TRUNK_RING;        // ring slots per worker wave (TRING - 1 items in flight)
 constexpr unsigned long long TIMEOUT_TICKS = 20000000ull;   // 200 ms of the 100 MHz real-time clock
-constexpr int HD = 128;                     // head_dim
-constexpr int RMAX = 4;                     // query heads per kv head
+// head_dim D (64 or 128) and the most query heads per kv head RMAX (4 or 8) are
+// template parameters of the kernel: (128, 4) for the Llama-3 shapes, (64, 8) for
+// TinyLlama's
 
 constexpr int NT = 6;                       // ops per layer, in this order:
 enum OpKind { K_QKV = 0, K_ATTN = 1, K_MERGE = 2, K_O = 3, K_GU = 4, K_DOWN = 5 };
@@ -219,15 +220,17 @@ __device__ __forceinline__ AttnUnit attn_unit(const Args &a, int wg, int T, int 
 
 using namespace step;
 
-template <int BITS>
+template <int BITS, int D, int RMAX>
 __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
+    static_assert(D == 64 || D == 128, "head_dim");
+    static_assert(RMAX <= 16, "query heads per kv head (one MFMA tile of columns)");
     constexpr int SPAN_K = BITS == 4 ? 128 : 64;
     constexpr int SPAN_GROUPS = SPAN_K / 64;
     constexpr int SPAN_WORDS = SPAN_K / 8;
     constexpr int ITEM_K = 4 * SPAN_K;
     constexpr int ITEM_GROUPS = ITEM_K / 64;
     constexpr int MFMAS = BITS == 4 ? 4 : 2;
-    constexpr int D = HD;
+    constexpr int KCH = D / 8;              // 16-byte chunks of a key row
     constexpr int AST = RMAX * (D + 4);     // floats per attention item state: [RMAX][D + 4] = O, m, l, pad
 
     extern __shared__ __align__(16) uint8_t smem[];
@@ -630,7 +633,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 if (au.valid) {
                     const int rpos = pos + a.pos_offset;
                     const float *ct = a.cos_t + (size_t)rpos * (D / 2), *st = a.sin_t + (size_t)rpos * (D / 2);
-                    const float cv = ct[lane], sv = st[lane];     // loads overlap the poll
+                    const int li = lane < D / 2 ? lane : 0;
+                    const float cv = ct[li], sv = st[li];         // loads overlap the poll
                     const uint2 *src = a.buf[B_QKV];
                     const int qc = a.R * D / 8;                 // q chunks, then k (D / 8), then v (D / 8)
                     auto addr = [&](int c) -> const uint2 * {
@@ -647,21 +651,24 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     if (ok) {
                         // rotate the q heads and the new key in place (rope_append_kernel's
                         // arithmetic): lane = dim i of the first half, pairs (i, i + D/2)
-                        for (int h = 0; h <= a.R; ++h) {
-                            uint16_t *row = qkv_l + (h < a.R ? h * D : RMAX * D);
-                            const float x1 = bf2f(row[lane]), x2 = bf2f(row[lane + D / 2]);
-                            row[lane] = (uint16_t)f2bf(add_rn(mul_rn(x1, cv), mul_rn(-x2, sv)));
-                            row[lane + D / 2] = (uint16_t)f2bf(add_rn(mul_rn(x2, cv), mul_rn(x1, sv)));
+                        if (lane < D / 2) {
+                            for (int h = 0; h <= a.R; ++h) {
+                                uint16_t *row = qkv_l + (h < a.R ? h * D : RMAX * D);
+                                const float x1 = bf2f(row[lane]), x2 = bf2f(row[lane + D / 2]);
+                                row[lane] = (uint16_t)f2bf(add_rn(mul_rn(x1, cv), mul_rn(-x2, sv)));
+                                row[lane + D / 2] = (uint16_t)f2bf(add_rn(mul_rn(x2, cv), mul_rn(x1, sv)));
+                            }
                         }
                         // the unit holding the new position appends it to the cache
                         if (au.lo <= T - 1 && T - 1 < au.hi) {
                             uint16_t *kd = slp[l].kc + ((size_t)au.kvh * a.T_cap + (T - 1)) * D;
                             uint16_t *vd = slp[l].vt + (size_t)au.kvh * D * a.T_cap + (T - 1);
                             const uint16_t *kr = qkv_l + RMAX * D, *vr = qkv_l + RMAX * D + D;
-                            kd[lane] = kr[lane];
-                            kd[lane + 64] = kr[lane + 64];
-                            vd[(size_t)lane * a.T_cap] = vr[lane];
-                            vd[(size_t)(lane + 64) * a.T_cap] = vr[lane + 64];
+#pragma unroll
+                            for (int i = lane; i < D; i += 64) {
+                                kd[i] = kr[i];
+                                vd[(size_t)i * a.T_cap] = vr[i];
+                            }
                         }
                     }
                 }
@@ -835,16 +842,26 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             if (lane < 32)
                 dma16((lane < 16 ? lp.s[gi] : lp.b[gi]) + (wrow(lane & 15) * G + (uint32_t)((ch * ITEM_GROUPS) & ~7)), d4);
         } else {
-            // 8 cached keys: K rows [kb, kb + 8) (2 KB; row r's 16-byte chunks rotated by r, so
-            // the 8 rows' same chunk sits in different banks) and V^T columns (128 x 16 B)
+            // 8 cached keys: K rows [kb, kb + 8) (D 2 bytes each, from the slot's start; row r's
+            // 16-byte chunks rotated by r, so the 8 rows' same chunk sits in different banks)
+            // and V^T columns (D x 16 B, from byte 2048).  head_dim 64 fills half of each;
+            // the other instructions reload the same bytes, so every item issues five.
             const int kb = au.lo + 8 * w.i;
             const uint8_t *kp = reinterpret_cast<const uint8_t *>(lp.kc + ((size_t)au.kvh * a.T_cap + kb) * D);
             const uint16_t *vp = lp.vt + (size_t)au.kvh * D * a.T_cap + kb;
-            const int kr0 = lane >> 4, kr1 = 4 + (lane >> 4);
-            dma16(kp + kr0 * 256 + (((lane & 15) + kr0) & 15) * 16, dst);
-            dma16(kp + kr1 * 256 + (((lane & 15) + kr1) & 15) * 16, d1);
-            dma16(vp + (size_t)lane * a.T_cap, d2);
-            dma16(vp + (size_t)(64 + lane) * a.T_cap, d3);
+            if (D == 128) {
+                const int kr0 = lane >> 4, kr1 = 4 + (lane >> 4);
+                dma16(kp + kr0 * 256 + (((lane & 15) + kr0) & 15) * 16, dst);
+                dma16(kp + kr1 * 256 + (((lane & 15) + kr1) & 15) * 16, d1);
+                dma16(vp + (size_t)lane * a.T_cap, d2);
+                dma16(vp + (size_t)(64 + lane) * a.T_cap, d3);
+            } else {
+                const int kr = lane >> 3;
+                dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
+                dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
+                dma16(vp + (size_t)lane * a.T_cap, d2);
+                dma16(vp + (size_t)lane * a.T_cap, d2);
+            }
             if (lane < 32) dma16(kp + 16 * lane, d4);
         }
         return w;
@@ -961,12 +978,12 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             // masked, and MFMA rows do not mix).  The new key is not in the cache yet:
             // its rotated copy is in LDS.  Operand B: query head min(ac, R - 1), the same
             // chunk (columns past R are ignored).
-            const uint4 *krow = reinterpret_cast<const uint4 *>(sl + ac * 256);
+            const uint4 *krow = reinterpret_cast<const uint4 *>(sl + ac * (2 * D));
             const uint4 *qrow = reinterpret_cast<const uint4 *>(qkv_l + min(ac, R - 1) * D);
             uint4 kv[D / 32], qv[D / 32];
 #pragma unroll
             for (int u = 0; u < D / 32; ++u) {
-                kv[u] = krow[(4 * u + ag - ac) & 15];
+                kv[u] = krow[(4 * u + ag - ac) & (KCH - 1)];
                 qv[u] = qrow[4 * u + ag];
             }
             if (has_new) {
@@ -1112,6 +1129,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
 struct DecodePlan {
     int device = 0;
     int bits = 4;
+    int head_dim = 128;         // with RMAX 4 (128) or 8 (64)
     int P = 0;
     Args args{};
     LayerPtrs *d_layers = nullptr;
@@ -1129,9 +1147,11 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
               D = m->head_dim;
     if (m->bits != 4 && m->bits != 8) return set_error(SC_EUNSUPPORTED, "decode_plan: bits must be 4 or 8");
     if (m->group_size != 64) return set_error(SC_EUNSUPPORTED, "decode_plan: group size 64 only");
-    if (D != HD) return set_error(SC_EUNSUPPORTED, "decode_plan: head_dim %d (128 only)", D);
+    if (D != 128 && D != 64) return set_error(SC_EUNSUPPORTED, "decode_plan: head_dim %d (64 or 128)", D);
+    // query heads per kv head: up to 4 at head_dim 128, up to 8 at 64 (the kernels built)
+    const int RMAX = D == 128 ? 4 : 8;
     if (L <= 0 || H <= 0 || Hkv <= 0 || H % Hkv || H / Hkv > RMAX)
-        return set_error(SC_EUNSUPPORTED, "decode_plan: at most %d query heads per kv head", RMAX);
+        return set_error(SC_EUNSUPPORTED, "decode_plan: at most %d query heads per kv head at head_dim %d", RMAX, D);
     if (hid % 512 || I % 512 || (H * D) % 512)
         return set_error(SC_EUNSUPPORTED, "decode_plan: widths must be multiples of 512");
     if (hid > 16384 || I > 16384 || H * D > 16384)
@@ -1233,6 +1253,7 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     std::unique_ptr<DecodePlan> pl(new DecodePlan());
     pl->device = dev;
     pl->bits = m->bits;
+    pl->head_dim = D;
     pl->P = P;
     pl->lds = off;
     SC_HIP_CHECK(hipMalloc(&pl->d_mem, mem));
@@ -1279,9 +1300,9 @@ int decode_plan_run(void *plan, hipStream_t stream) {
     int dev = 0;
     SC_HIP_CHECK(hipGetDevice(&dev));
     if (dev != pl->device) return set_error(SC_EINVAL, "decode_plan_run: plan belongs to device %d", pl->device);
-    auto go = [&](auto kern) -> int {
-        static int configured[2] = {0, 0};
-        int &cfg = configured[pl->bits == 4 ? 0 : 1];
+    auto go = [&](auto kern, int variant) -> int {
+        static int configured[4] = {0, 0, 0, 0};
+        int &cfg = configured[variant];
         if ((int)pl->lds > cfg) {
             SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)pl->lds));
@@ -1295,8 +1316,12 @@ int decode_plan_run(void *plan, hipStream_t stream) {
         SC_HIP_CHECK(hipGetLastError());
         return SC_OK;
     };
-    if (pl->bits == 4) return go(decode_step_kernel<4>);
-    return go(decode_step_kernel<8>);
+    if (pl->head_dim == 128) {
+        if (pl->bits == 4) return go(decode_step_kernel<4, 128, 4>, 0);
+        return go(decode_step_kernel<8, 128, 4>, 1);
+    }
+    if (pl->bits == 4) return go(decode_step_kernel<4, 64, 8>, 2);
+    return go(decode_step_kernel<8, 64, 8>, 3);
 }
 
 int decode_plan_status(void *plan, unsigned *status) {

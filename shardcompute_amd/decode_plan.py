@@ -65,9 +65,10 @@ def eligible(model, cache) -> Tuple[bool, str]:
         return False, "quantized embedding"
     for layer in model.layers:
         att, mlp = layer.attention, layer.mlp
-        if not att.use_quantized or att.head_dim != 128:
+        if not att.use_quantized or att.head_dim not in (64, 128):
             return False, "head_dim"
-        if att.local_num_heads // att.local_num_kv_heads > 4:
+        # the kernels built: up to 4 query heads per kv head at head_dim 128, 8 at 64
+        if att.local_num_heads // att.local_num_kv_heads > (4 if att.head_dim == 128 else 8):
             return False, "query heads per kv head"
         if not all(_bias_free(x) for x in (att.q_proj, att.k_proj, att.v_proj, att.o_proj)):
             return False, "attention linear bias"

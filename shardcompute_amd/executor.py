@@ -275,6 +275,8 @@ class ParallelExecutor:
         if temperature == 0:
             dec = DecodeGraph(self.model, cache, tokens, use_graph=self.use_graphs)
             plan = dec.bufs.plan
+            # which decode path ran: "trunk" (one launch per token) or "per-op"
+            self.last_decode_path = "trunk" if plan is not None else "per-op"
 
             def check_plan():
                 # the whole-trunk launch bounds every wait; one that gave up left its

@@ -82,15 +82,12 @@ def test_tinyllama_greedy_128_tokens(device):
     out = run(ex.generate(torch.from_numpy(prompt).cuda(), max_new_tokens=128, temperature=0.0))
     new = out[0, 32:].cpu().numpy()
     assert new.shape == (128,)
-    # logits of every step from the GPU's own decode, teacher-forced on the same tokens
-    cache = model.new_cache(1, 256)
-    logits, _ = run(model.forward(torch.from_numpy(prompt).cuda(), past_key_values=cache, use_cache=True,
-                                  last_only=True))
-    gl = [f32(logits)[0]]
-    for t in range(127):
-        lg, _ = run(model.forward(torch.tensor([[int(new[t])]], device="cuda"), past_key_values=cache,
-                                  use_cache=True))
-        gl.append(f32(lg)[0])
+    assert ex.last_decode_path == "trunk"           # head_dim 64, 8 q heads per kv head: one launch per token
+    # logits of every step from the GPU's own decode path (the whole-trunk launch and
+    # the lm_head), teacher-forced on the same tokens: the same kernels on the same
+    # inputs, so the same bits as during generation
+    _, lgs = _decode_logits(model, torch.from_numpy(prompt).cuda(), 128, forced=new[None, :])
+    gl = [lg[0] for lg in lgs]
     print("  oracle teacher-forced run", flush=True)
     _, ol = oracle.generate_greedy(prompt, 128, forced=new[None, :])
     errs = [rel(g, o[0]) for g, o in zip(gl, ol)]

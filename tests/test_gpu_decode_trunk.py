@@ -139,6 +139,25 @@ def test_eligibility(small_w4):
     assert eligible(m, m.new_cache(2, 64))[0] is False
 
 
+TINY = dict(hidden=2048, inter=5632, heads=32, kv_heads=4, vocab=2048, layers=3)
+
+
+@pytest.fixture(scope="module")
+def tiny_w4():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    return build(TINY, 4, 512, seed=7)
+
+
+@pytest.mark.parametrize("prompt_len", [1, 37, 300])
+def test_trunk_matches_per_op_tinyllama_heads(tiny_w4, prompt_len):
+    # head_dim 64, 8 query heads per kv head, 64 key ranges per kv head on 256 CUs
+    assert eligible(tiny_w4, tiny_w4.new_cache(1, 64)) == (True, "")
+    print(f"trunk vs per-op: W4 TinyLlama heads, prompt {prompt_len}", flush=True)
+    worst = compare_paths(tiny_w4, prompt_len, steps=6, capacity=512)
+    print(f"  worst logits max-abs-rel {worst:.2e}", flush=True)
+
+
 @pytest.mark.parametrize("prompt_len", [1, 37, 300])
 def test_trunk_matches_per_op_w4(small_w4, prompt_len):
     print(f"trunk vs per-op: W4 small, prompt {prompt_len}", flush=True)

@@ -219,6 +219,25 @@ def test_c_restatement_matches_numpy(clib, bits, M):
         assert d.max() <= 1 and (d > 0).mean() < 1e-3
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 96), (7, 2048, 33), (40, 512, 130)])
+def test_fast_cpu_restatement_matches_oracle(clib, bits, M, K, N):
+    # the vectorised fp32 restatement timed as the CPU baseline computes the same
+    # product: within 2 bf16 steps of the fp64 oracle (fp32 accumulation), the bias
+    # added after rounding
+    rng = np.random.default_rng(30 + bits + M)
+    x, wq, s, b = _rand_case(rng, M, K, N, bits)
+    bias = f32_to_bf16(rng.standard_normal(N).astype(np.float32))
+    for bb in (None, bias):
+        yf = cref.qmm_fast_bf16(x, wq, s, b, bb, 64, bits, threads=4)
+        yr = quantized_matmul_bf16(x, wq, s, b, bb, 64, bits)
+        ref = bf16_to_f32(yr).astype(np.float64)
+        err = np.abs(bf16_to_f32(yf).astype(np.float64) - ref)
+        assert err.max() <= 1e-2 * np.abs(ref).max()
+        d = np.abs(yf.astype(np.int32) - yr.astype(np.int32))
+        assert (d > 2).mean() < 1e-3
+
+
 # ---------------------------------------------------------------- quantizer
 
 @pytest.mark.parametrize("bits", [4, 8])
