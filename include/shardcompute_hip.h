@@ -312,6 +312,31 @@ int sc_attention_decode_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B,
  */
 int sc_silu_mul_bf16(const uint16_t *gate_up, int64_t rows, int64_t I, uint16_t *out, void *hip_stream);
 
+/* Activation kinds of sc_act_bf16 (ParallelMLP's activation names). */
+#define SC_ACT_SILU 0       /* "silu" / "swish": x / (1 + exp(-x))                        */
+#define SC_ACT_GELU 1       /* "gelu": x * sigmoid(1.702 x)                               */
+#define SC_ACT_GELU_NEW 2   /* "gelu_new": 0.5 x (1 + tanh(0.79788456 (x + 0.044715 x^3))) */
+#define SC_ACT_RELU 3       /* "relu": max(x, 0)                                          */
+#define SC_ACT_GELU_EXACT 4 /* "gelu_exact": 0.5 x (1 + erf(x / sqrt(2)))                 */
+
+/*
+ * The MLP activation of any kind: gated, out[rows, I] = f(gate) * up for
+ * in = gate|up [rows, 2I] (gate columns first); ungated, out[rows, I] = f(in[rows, I])
+ * (out may equal in).  fp32 arithmetic, one bf16 rounding.  I a multiple of 8,
+ * 16-byte aligned pointers.  Replaces the activation step of ParallelMLP.forward,
+ * gated and ungated, for every activation it accepts:
+ *   src/shardcompute/parallel/mlp.py:159-180 (the activations), :236-250 (their use).
+ */
+int sc_act_bf16(const uint16_t *in, int64_t rows, int64_t I, int kind, int gated, uint16_t *out, void *hip_stream);
+
+/*
+ * out[r, d] = bf16(x[r, d] + bias[d]) for x [rows, D] (out may equal x): the
+ * LayerNorm-style bias of RMSNorm.__call__, src/shardcompute/parallel/transformer.py:
+ * 57-59, added to the normalised, scaled row.  D a multiple of 8, 16-byte aligned.
+ */
+int sc_add_row_bias_bf16(const uint16_t *x, int64_t rows, int64_t D, const uint16_t *bias, uint16_t *out,
+                         void *hip_stream);
+
 /*
  * ids[r] = first index of the maximum of logits row r (NaN counts as the maximum,
  * -0.0 equals +0.0).  When tokens_or_null is given the id is also stored at

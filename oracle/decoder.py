@@ -9,8 +9,10 @@ Follows the reference's per-rank forward at world_size = 1:
 * ``attention``      ``parallel/attention.py:403-471`` (QKV, RoPE, KV concat,
   GQA repeat, ``q k^T / sqrt(d)``, causal ``triu(k = kv - s + 1)``, softmax, ``@ v``,
   o_proj)
-* ``mlp``            ``parallel/mlp.py:238-254`` (``down(silu(gate(x)) * up(x))``,
-  ``silu(x) = x * sigmoid(x)`` at ``:161-162``)
+* ``mlp``            ``parallel/mlp.py:238-254`` (gated ``down(f(gate(x)) * up(x))``,
+  ungated ``down(f(up(x)))``; the activations f of ``:159-180``: silu/swish,
+  gelu = ``x * sigmoid(1.702 x)``, gelu_new (tanh form), relu, gelu_exact (erf))
+* ``rms_norm`` with the optional LayerNorm-style bias of ``transformer.py:57-59``
 * ``block``          ``parallel/transformer.py:237-254`` (pre-norm residual block)
 * ``forward``        ``parallel/transformer.py:536-577`` (embed, layers, norm, lm_head)
 * ``generate_greedy`` ``worker/executor.py:229-347`` with temperature 0
@@ -66,6 +68,8 @@ class DecoderShape:
     rope_theta: float = 10000.0
     bits: int = 4
     group_size: int = 64
+    activation: str = "silu"       # ParallelMLP's activation name
+    gated: bool = True             # gate/up/down (Llama) or up/down (fc1/fc2)
 
     def __post_init__(self):
         if not self.head_dim:
@@ -100,12 +104,16 @@ def qlinear(x32, lin: QLinear, shape: DecoderShape):
     return y.reshape(lead + (w.shape[0],))
 
 
-def rms_norm(x32, w_bf16, eps):
-    """``(x / sqrt(mean(x*x) + eps)) * w`` in fp32, rounded once to bf16."""
+def rms_norm(x32, w_bf16, eps, bias_bf16=None):
+    """``(x / sqrt(mean(x*x) + eps)) * w`` in fp32, rounded once to bf16; with a
+    LayerNorm-style bias (``transformer.py:57-59``) the bias is added to that bf16 row
+    and the sum rounded again."""
     x = x32.astype(np.float32)
     ms = np.mean(x * x, axis=-1, keepdims=True, dtype=np.float32)
-    y = (x / np.sqrt(ms + np.float32(eps))) * bf16_to_f32(w_bf16)
-    return round_bf16(y)
+    y = round_bf16((x / np.sqrt(ms + np.float32(eps))) * bf16_to_f32(w_bf16))
+    if bias_bf16 is not None:
+        y = round_bf16(y + bf16_to_f32(bias_bf16))
+    return y
 
 
 def rope_cos_sin(positions, head_dim, base):
@@ -133,6 +141,35 @@ def silu(x32):
     x = np.asarray(x32, dtype=np.float32)
     with np.errstate(over="ignore"):
         return x / (np.float32(1) + np.exp(-x, dtype=np.float32))
+
+
+def activation(x32, name):
+    """The MLP activations of ``parallel/mlp.py:159-180`` in fp32 (the op order of
+    the formulas there; the GPU kernel follows the same order):
+
+    * ``silu`` / ``swish``: ``x / (1 + exp(-x))`` (= ``x * sigmoid(x)``)
+    * ``gelu``:        ``x / (1 + exp(-1.702 x))`` (= ``x * sigmoid(1.702 x)``)
+    * ``gelu_new``:    ``0.5 x (1 + tanh(0.7978845608028654 (x + 0.044715 x^3)))``
+    * ``relu``:        ``max(x, 0)``, NaN kept (``mx.maximum``)
+    * ``gelu_exact``:  ``0.5 x (1 + erf(x / sqrt(2)))``
+    """
+    x = np.asarray(x32, dtype=np.float32)
+    f = np.float32
+    with np.errstate(over="ignore", invalid="ignore"):
+        if name in ("silu", "swish"):
+            return silu(x)
+        if name == "gelu":
+            return x / (f(1) + np.exp(f(-1.702) * x, dtype=np.float32))
+        if name == "gelu_new":
+            t = np.tanh(f(0.7978845608028654) * (x + f(0.044715) * ((x * x) * x)), dtype=np.float32)
+            return (f(0.5) * x) * (f(1) + t)
+        if name == "relu":
+            return np.where((x > 0) | np.isnan(x), x, f(0))
+        if name == "gelu_exact":
+            from scipy.special import erf
+            e = erf(x * f(0.7071067811865476)).astype(np.float32)
+            return (f(0.5) * x) * (f(1) + e)
+    raise ValueError(f"Unknown activation: {name}")
 
 
 def attention_core(q, k, v, scale, causal_offset, mask=None):
@@ -200,9 +237,12 @@ class OracleDecoder:
 
     def _mlp(self, x, L):
         sh = self.shape
-        g = qlinear(x, L["gate"], sh)
         u = qlinear(x, L["up"], sh)
-        a = round_bf16(silu(g) * u)
+        if sh.gated:
+            g = qlinear(x, L["gate"], sh)
+            a = round_bf16(activation(g, sh.activation) * u)
+        else:
+            a = round_bf16(activation(u, sh.activation))
         return qlinear(a, L["down"], sh)
 
     def forward(self, ids, last_only=False, mask=None):
@@ -213,13 +253,13 @@ class OracleDecoder:
         ids = np.asarray(ids)
         h = bf16_to_f32(vocab_gather_bf16(ids, self.w["embed"], 0))
         for li, L in enumerate(self.w["layers"]):
-            xn = rms_norm(h, L["input_ln"], sh.rms_norm_eps)
+            xn = rms_norm(h, L["input_ln"], sh.rms_norm_eps, L.get("input_ln_bias"))
             h = round_bf16(h + self._attn(li, xn, L, mask=mask))
-            xn = rms_norm(h, L["post_ln"], sh.rms_norm_eps)
+            xn = rms_norm(h, L["post_ln"], sh.rms_norm_eps, L.get("post_ln_bias"))
             h = round_bf16(h + self._mlp(xn, L))
         if last_only:
             h = h[:, -1:]
-        hn = rms_norm(h, self.w["norm"], sh.rms_norm_eps)
+        hn = rms_norm(h, self.w["norm"], sh.rms_norm_eps, self.w.get("norm_bias"))
         return qlinear(hn, self.w["lm_head"], sh)
 
     def generate_greedy(self, ids, max_new_tokens, forced=None):

@@ -40,6 +40,8 @@ EXPORTS = (
     "sc_attention_decode_workspace_bytes",
     "sc_attention_decode_bf16",
     "sc_silu_mul_bf16",
+    "sc_act_bf16",
+    "sc_add_row_bias_bf16",
     "sc_argmax_bf16",
     "sc_add_bf16",
     "sc_add_i32",
@@ -119,6 +121,10 @@ def load():
         lib.sc_attention_decode_bf16.restype = i32
         lib.sc_silu_mul_bf16.argtypes = [p, i64, i64, p, p]
         lib.sc_silu_mul_bf16.restype = i32
+        lib.sc_act_bf16.argtypes = [p, i64, i64, i32, i32, p, p]
+        lib.sc_act_bf16.restype = i32
+        lib.sc_add_row_bias_bf16.argtypes = [p, i64, i64, p, p, p]
+        lib.sc_add_row_bias_bf16.restype = i32
         lib.sc_argmax_bf16.argtypes = [p, i64, i64, p, p, i64, i64, p, p]
         lib.sc_argmax_bf16.restype = i32
         lib.sc_add_bf16.argtypes = [p, p, p, i64, p]
@@ -617,6 +623,47 @@ def silu_mul(gate_up, out=None):
         out = torch.empty(gate_up.shape[:-1] + (I,), dtype=torch.bfloat16, device=gate_up.device)
     rc = lib.sc_silu_mul_bf16(_ptr(gate_up), rows, I, _ptr(out), _stream(gate_up))
     _check(rc, "sc_silu_mul_bf16")
+    return out
+
+
+ACT_KINDS = {"silu": 0, "swish": 0, "gelu": 1, "gelu_new": 2, "relu": 3, "gelu_exact": 4}
+
+
+def act(x, activation, gated, out=None):
+    """The MLP activation by name (``ParallelMLP``'s names): gated, f(gate) * up for
+    x = gate|up [..., 2I] -> [..., I]; ungated, f(x) for x [..., I] -> [..., I]."""
+    lib = load()
+    _require_gpu(x, out)
+    _bf16(x, "x")
+    if activation not in ACT_KINDS:
+        raise ValueError(f"Unknown activation: {activation}")
+    x = x.contiguous()
+    W = x.shape[-1]
+    if gated and W % 2:
+        raise ValueError("gate_up width must be even")
+    I = W // 2 if gated else W
+    rows = x.numel() // W if W else 0
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (I,), dtype=torch.bfloat16, device=x.device)
+    rc = lib.sc_act_bf16(_ptr(x), rows, I, ACT_KINDS[activation], 1 if gated else 0, _ptr(out), _stream(x))
+    _check(rc, "sc_act_bf16")
+    return out
+
+
+def add_row_bias(x, bias, out=None):
+    """x [..., D] + bias [D] per row, rounded to bf16 (out may be x)."""
+    lib = load()
+    _require_gpu(x, bias, out)
+    _bf16(x, "x"), _bf16(bias, "bias")
+    x = x.contiguous()
+    D = x.shape[-1]
+    if tuple(bias.shape) != (D,):
+        raise ValueError(f"bias must be [{D}], got {tuple(bias.shape)}")
+    if out is None:
+        out = torch.empty_like(x)
+    rows = x.numel() // D if D else 0
+    rc = lib.sc_add_row_bias_bf16(_ptr(x), rows, D, _ptr(bias.contiguous()), _ptr(out), _stream(x))
+    _check(rc, "sc_add_row_bias_bf16")
     return out
 
 

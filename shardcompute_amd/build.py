@@ -19,7 +19,7 @@ BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libshardcompute_hip.so")
 ARCH = os.environ.get("SC_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["abi.hip", "qgemv_dma.hip", "qgemv_m1.hip", "qgemv16.hip", "qgemv.hip", "qgemm.hip", "qgemm_band.hip", "gather.hip", "quant.hip", "decode.hip", "attn_prefill.hip", "decode_step.hip"]
+SOURCES = ["abi.hip", "qgemv_dma.hip", "qgemv_m1.hip", "qgemv16.hip", "qgemv.hip", "qgemm.hip", "qgemm_band.hip", "gather.hip", "quant.hip", "decode.hip", "attn_prefill.hip", "decode_step.hip", "act.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

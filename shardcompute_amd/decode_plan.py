@@ -72,8 +72,10 @@ def eligible(model, cache) -> Tuple[bool, str]:
             return False, "query heads per kv head"
         if not all(_bias_free(x) for x in (att.q_proj, att.k_proj, att.v_proj, att.o_proj)):
             return False, "attention linear bias"
-        if not mlp.use_gated or mlp.activation_name != "silu":
+        if not mlp.fused_swiglu:
             return False, "MLP activation"
+        if not (layer.input_layernorm.fusable and layer.post_attention_layernorm.fusable):
+            return False, "norm bias"
         if not all(_bias_free(x) for x in (mlp.gate_proj, mlp.up_proj, mlp.down_proj)):
             return False, "MLP linear bias"
         bits = {att.q_proj.bits, att.o_proj.bits, mlp.gate_proj.bits, mlp.down_proj.bits}

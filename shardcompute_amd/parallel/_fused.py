@@ -100,11 +100,11 @@ class FusedColumns:
         if not self._current():
             self.build()
         norm._check()
-        if self.quantized:
+        if self.quantized and norm.fusable:
             return _lib.qmm_rmsnorm(h, norm.weight, norm.eps, self._wq, self._s, self._b, residual=residual,
                                     h_out=h_out, xn_out=xn_out, bias=self._bias, bits=self.bits,
                                     group_size=self.group_size, out=out)
-        xn = _lib.rms_norm(h, norm.weight, norm.eps, residual=residual, h_out=h_out, out=xn_out)
+        xn = norm(h, residual=residual, h_out=h_out, out=xn_out)
         return self(xn, out=out), xn
 
     def swiglu_call(self, h, norm=None, residual=None, h_out=None, xn_out=None, act_out=None, gu_out=None):
@@ -117,13 +117,13 @@ class FusedColumns:
             raise ValueError("swiglu needs a gate|up pair of equal widths")
         if norm is not None:
             norm._check()
-        if self.quantized:
+        if self.quantized and (norm is None or norm.fusable):
             act, _ = _lib.qmm_swiglu(h, self._wq, self._s, self._b, norm_weight=norm.weight if norm else None,
                                      eps=norm.eps if norm else 1e-5, residual=residual, h_out=h_out,
                                      xn_out=xn_out, bias=self._bias, bits=self.bits, group_size=self.group_size,
                                      act_out=act_out, gate_up_scratch=gu_out)
             return act
-        xn = _lib.rms_norm(h, norm.weight, norm.eps, residual=residual, h_out=h_out, out=xn_out) if norm else h
+        xn = norm(h, residual=residual, h_out=h_out, out=xn_out) if norm else h
         return _lib.silu_mul(self(xn, out=gu_out), out=act_out)
 
     def split(self, y):

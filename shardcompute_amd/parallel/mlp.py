@@ -1,13 +1,13 @@
-"""Tensor-parallel gated MLP over the HIP kernels.
+"""Tensor-parallel MLP over the HIP kernels.
 
 Drop-in for ``ParallelMLP`` of ``src/shardcompute/parallel/mlp.py:18-279``:
-``down(silu(gate(x)) * up(x))`` (``:228-254``).  gate and up run as one fused
-quantized product (bit-identical per column), ``sc_silu_mul_bf16`` applies
-``silu(g) = g / (1 + exp(-g))`` times up, and the row-parallel down projection
-finishes (all-reduce = identity at world_size 1).  The kernels implement the
-gated SiLU/swish MLP the reference's Llama-family models use; the other
-activation names of ``:159-177`` and the ungated variant raise
-``NotImplementedError``.
+gated, ``down(f(gate(x)) * up(x))``; ungated, ``down(f(up(x)))`` (``:228-254``),
+with f any activation the reference accepts (``silu``/``swish``, ``gelu``,
+``gelu_new``, ``relu``, ``gelu_exact``, ``:159-180``).  gate and up run as one
+fused quantized product (bit-identical per column); the gated SiLU, the Llama
+family's MLP, applies silu(gate) * up inside that product's kernel; every other
+form runs the product, ``sc_act_bf16`` and the row-parallel down projection
+(all-reduce = identity at world_size 1).
 """
 import logging
 from typing import Optional
@@ -80,21 +80,34 @@ class ParallelMLP:
         if self.use_gated and gate_weight is not None:
             self.gate_proj.load_quantized_shard(gate_weight, gate_scales, gate_biases, gate_linear_bias)
 
-    def _check_supported(self):
-        if not self.use_gated or self.activation_name not in _SUPPORTED:
-            raise NotImplementedError(f"the HIP MLP implements the gated silu MLP; got use_gated={self.use_gated}, "
-                                      f"activation={self.activation_name!r}")
+    @property
+    def fused_swiglu(self) -> bool:
+        """The gated SiLU MLP: its gate|up product applies the activation itself."""
+        return self.use_gated and self.activation_name in _SUPPORTED
 
     def intermediate(self, x2, gu_out=None, out=None):
-        """silu(gate(x)) * up(x) for x2 ``[rows, hidden]`` -> ``[rows, local_intermediate]``."""
-        self._check_supported()
-        gu = self.gate_up(x2, out=gu_out)
-        return _lib.silu_mul(gu, out=out)
+        """f(gate(x)) * up(x) (gated) or f(up(x)) for x2 ``[rows, hidden]`` ->
+        ``[rows, local_intermediate]``."""
+        if self.use_gated:
+            gu = self.gate_up(x2, out=gu_out)
+            return _lib.act(gu, self.activation_name, gated=True, out=out)
+        return _lib.act(self.up_proj.forward_sync(x2), self.activation_name, gated=False, out=out)
+
+    def act_call(self, h, norm, residual=None, h_out=None, xn_out=None, act_out=None, gu_out=None):
+        """The activation of the MLP's input projections applied to norm(h + residual)
+        (``transformer.py:249-253``); the residual sum goes to ``h_out``.  The gated SiLU
+        with a bias-free norm runs as one kernel (norm, gate|up, SiLU gate)."""
+        if self.fused_swiglu:
+            return self.gate_up.swiglu_call(h, norm, residual=residual, h_out=h_out, xn_out=xn_out,
+                                            act_out=act_out, gu_out=gu_out)
+        xn = norm(h, residual=residual, h_out=h_out, out=xn_out)
+        return self.intermediate(xn, gu_out=gu_out, out=act_out)
 
     async def down_from_gate_up(self, gate_up, act_out=None):
-        """down(silu(gate) * up) from the fused gate|up product."""
-        self._check_supported()
-        return await self.down_proj.forward(_lib.silu_mul(gate_up, out=act_out))
+        """down(f(gate) * up) from the fused gate|up product (gated MLPs)."""
+        if not self.use_gated:
+            raise ValueError("down_from_gate_up needs a gated MLP")
+        return await self.down_proj.forward(_lib.act(gate_up, self.activation_name, gated=True, out=act_out))
 
     async def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
         lead = hidden_states.shape[:-1]

@@ -78,14 +78,23 @@ class RMSNorm:
     def _check(self):
         if self.weight is None:
             raise RuntimeError("Weights not loaded")
-        if self.bias is not None:
-            raise NotImplementedError("LayerNorm-style bias is not supported by the HIP RMSNorm kernel")
+
+    @property
+    def fusable(self) -> bool:
+        """Whether the projections that read this norm may normalise inside their own
+        kernel (they take no LayerNorm-style bias; with one the norm runs on its own)."""
+        return self.bias is None
 
     def __call__(self, x, residual=None, h_out=None, out=None):
-        """``(x / sqrt(mean(x^2) + eps)) * weight``; with ``residual`` the input is
+        """``(x / sqrt(mean(x^2) + eps)) * weight``, then ``+ bias`` when one is loaded
+        (LayerNorm-style, ``transformer.py:57-59``: the bias is added to the rounded
+        normalised row and rounded again); with ``residual`` the input is
         ``x + residual`` (written to ``h_out`` when given)."""
         self._check()
-        return _lib.rms_norm(x, self.weight, self.eps, residual=residual, h_out=h_out, out=out)
+        y = _lib.rms_norm(x, self.weight, self.eps, residual=residual, h_out=h_out, out=out)
+        if self.bias is not None:
+            y = _lib.add_row_bias(y, self.bias, out=y)
+        return y
 
 
 class ParallelTransformerBlock:
@@ -307,11 +316,10 @@ class ParallelTransformer:
             a = att.attend_qkv(qkv, B, S, cache[i], out=bufs.attn if bufs else None,
                                workspace=bufs.workspace if bufs else None, mask=mask)
             o = await att.o_proj.forward(a)
-            mlp._check_supported()
-            act = mlp.gate_up.swiglu_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
-                                          xn_out=bufs.xn if bufs is not None else None,
-                                          act_out=bufs.act if bufs is not None else None,
-                                          gu_out=bufs.gu if bufs is not None else None)
+            act = mlp.act_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
+                               xn_out=bufs.xn if bufs is not None else None,
+                               act_out=bufs.act if bufs is not None else None,
+                               gu_out=bufs.gu if bufs is not None else None)
             h, h_alt = h_alt, h
             pending = await mlp.down_proj.forward(act)
         return h, pending
@@ -323,7 +331,7 @@ class ParallelTransformer:
             if pending is not None:
                 pending = pending.reshape(B, S, -1)[:, -1].contiguous()
         lm = self.lm_head
-        if isinstance(lm, QuantizedColumnParallelLinear):
+        if isinstance(lm, QuantizedColumnParallelLinear) and self.norm.fusable:
             if lm.quantized_weight is None:
                 raise RuntimeError("Weight not loaded")
             self.norm._check()
@@ -390,7 +398,8 @@ class ParallelTransformer:
             h = self._embed_sync(bufs.ids, out=bufs.h.view(B, 1, self.hidden_size)).view(B, self.hidden_size)
             h, pending = run_sync(self._trunk(h, cache, B, 1, bufs))
         lm = self.lm_head
-        if isinstance(lm, QuantizedColumnParallelLinear) and (not lm.gather_output or self.world_size == 1):
+        if (isinstance(lm, QuantizedColumnParallelLinear) and (not lm.gather_output or self.world_size == 1)
+                and self.norm.fusable):
             # final norm, lm_head, greedy selection and counter advance in one call
             # (at batch 1 the lm_head GEMV selects the token while writing the logits)
             if lm.quantized_weight is None:

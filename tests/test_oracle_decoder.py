@@ -329,3 +329,63 @@ def test_attention_mask_log2_doubles_a_key():
     dup = [0, 1, 2, 2, 3, 4, 5, 6, 7, 8]
     ref = attention_core(q, k[:, :, dup], v[:, :, dup], 0.35, 9)
     assert np.allclose(got, ref, atol=1e-6, rtol=0)
+
+
+# ---------------------------------------------------------------- the other MLP and norm forms
+
+def test_activation_closed_forms_and_library():
+    import math
+    from oracle.decoder import activation
+    x = np.linspace(-6, 6, 2001).astype(np.float32)
+    x64 = x.astype(np.float64)
+    exact = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in x64])    # Python's math.erf
+    ge = activation(x, "gelu_exact")
+    assert np.abs(ge - exact).max() <= 2e-6 * max(1.0, np.abs(exact).max())
+    # the tanh form is within 5e-4 of the exact GELU (its published accuracy), the
+    # sigmoid form within 0.021; a wrong constant misses either bound
+    assert np.abs(activation(x, "gelu_new") - exact).max() <= 5e-4
+    assert np.abs(activation(x, "gelu") - exact).max() <= 0.021
+    assert np.abs(activation(x, "gelu") - x64 / (1 + np.exp(-1.702 * x64))).max() <= 1e-6 * 6
+    t = np.tanh(0.7978845608028654 * (x64 + 0.044715 * x64 ** 3))
+    assert np.abs(activation(x, "gelu_new") - 0.5 * x64 * (1 + t)).max() <= 2e-6 * 6
+    for name in ("gelu", "gelu_new", "gelu_exact", "silu", "swish"):
+        y = activation(np.array([0.0, 30.0, -30.0], np.float32), name)
+        assert y[0] == 0.0 and abs(y[1] - 30.0) < 1e-4 and abs(y[2]) < 1e-3
+    r = activation(np.array([-2.0, -0.0, 0.0, 3.0, np.nan], np.float32), "relu")
+    assert r[0] == 0.0 and r[1] == 0.0 and r[2] == 0.0 and r[3] == 3.0 and np.isnan(r[4])
+    assert np.array_equal(activation(x, "swish"), activation(x, "silu"))
+    import pytest
+    with pytest.raises(ValueError):
+        activation(x, "tanh")
+
+
+def test_rms_norm_bias_is_added_after_rounding():
+    rng = np.random.default_rng(40)
+    x = round_bf16(rng.standard_normal((3, 64)).astype(np.float32) * 3)
+    w = f32_to_bf16((1 + 0.1 * rng.standard_normal(64)).astype(np.float32))
+    b = f32_to_bf16((0.5 * rng.standard_normal(64)).astype(np.float32))
+    y0 = rms_norm(x, w, 1e-5)
+    assert np.array_equal(rms_norm(x, w, 1e-5, b), round_bf16(y0 + bf16_to_f32(b)))
+    # constant rows: the normalised row is w (closed form), plus the bias
+    c = np.full((2, 64), 2.5, np.float32)
+    exp = bf16_to_f32(w).astype(np.float64) * 2.5 / np.sqrt(2.5 ** 2 + 1e-5) + bf16_to_f32(b)
+    assert np.abs(rms_norm(c, w, 1e-5, b) - exp).max() <= 2 ** -7 * np.abs(exp).max()
+
+
+def test_ungated_and_other_activation_mlp_roles():
+    from oracle.decoder import activation
+    rng = np.random.default_rng(41)
+    sh, W = _one_layer_weights(rng)                  # gate = 2I, up = I, down = I
+    L = W["layers"][0]
+    x = round_bf16(np.stack([np.linspace(-4, 2, H64), rng.uniform(-4, 2, H64)]).astype(np.float32))
+    xd = x.astype(np.float64)
+    for name in ("gelu", "gelu_new", "relu", "gelu_exact"):
+        sh.activation, sh.gated = name, True
+        got = OracleDecoder(sh, W)._mlp(x, L)
+        f2 = activation((2 * x).astype(np.float32), name).astype(np.float64)
+        assert _close(got, f2 * xd, 1e-2), name                          # f(gate) * up
+        sh.gated = False
+        got = OracleDecoder(sh, W)._mlp(x, L)
+        f1 = activation(x, name).astype(np.float64)
+        assert _close(got, f1, 1e-2), name                               # f(up), the gate ignored
+        assert not _close(got, f2 * xd, 0.1), name

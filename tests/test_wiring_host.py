@@ -78,9 +78,15 @@ def test_mlp_constructor_validation():
         ParallelMLP(4096, 14335, 2, 0, None)
     with pytest.raises(ValueError):
         ParallelMLP(4096, 14336, 1, 0, None, activation="tanhh")
-    g = ParallelMLP(64, 128, 1, 0, None, activation="gelu", use_quantized=True)
-    with pytest.raises(NotImplementedError):
-        g.intermediate(torch.zeros(1, 64))
+    # every activation the reference accepts constructs, gated or not; only the gated
+    # SiLU runs fused into the gate|up product
+    for act in ("silu", "swish", "gelu", "gelu_new", "relu", "gelu_exact"):
+        for gated in (True, False):
+            g = ParallelMLP(64, 128, 1, 0, None, activation=act, use_gated=gated, use_quantized=True)
+            assert g.fused_swiglu == (gated and act in ("silu", "swish"))
+            assert (g.gate_up is None) == (not gated)
+    with pytest.raises(RuntimeError, match="Weight not loaded"):
+        ParallelMLP(64, 128, 1, 0, None, activation="gelu", use_quantized=True).intermediate(torch.zeros(1, 64))
 
 
 def test_transformer_construction_defaults():
