@@ -14,7 +14,7 @@
  *    -2 unsupported configuration, -3 HIP runtime error); sc_last_error() then
  *    holds a message (thread-local, valid until the next failing call).
  *  - The kernels allocate nothing per call.  The split-K path of sc_qmm_bf16 (and of
- *    the products inside sc_qmm_rmsnorm_bf16 / sc_qmm_swiglu_bf16 at 9-32 rows) uses a
+ *    the products inside sc_qmm_rmsnorm_bf16 / sc_qmm_swiglu_bf16 at 9-160 rows) uses a
  *    library-owned scratch per device, allocated on first need and grown (with a
  *    device synchronisation) when a larger shape arrives: calls that overlap on one
  *    device (concurrent streams) race on it, and the first call of a new largest
@@ -33,7 +33,8 @@ extern "C" {
 #define SC_ABI_VERSION 11
 
 /* Kernel selection for sc_qmm_bf16_path. */
-#define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV; 33-160: band kernel; above: GEMM     */
+#define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV or band kernel (by shape); 33-160:
+                              band kernel; above: GEMM                          */
 #define SC_QMM_PATH_GEMV 1 /* fused dequant-GEMV (decode batches, M <= 32)      */
 #define SC_QMM_PATH_GEMM 2 /* LDS-staged dequant -> bf16 MFMA GEMM (prefill)     */
 #define SC_QMM_PATH_BAND 3 /* weight-streaming band kernel (M <= 256)            */
@@ -89,8 +90,8 @@ int sc_qmm_bf16_band(const uint16_t *x, const uint32_t *wq, const uint16_t *scal
  * hipMalloc: code under HIP graph capture, tight serving loops, harnesses that
  * forbid allocation.  No counterpart in the reference (mx.quantized_matmul
  * allocates its output; this entry point allocates nothing at all).  Same
- * arguments, kernels and results as sc_qmm_bf16, bit for bit.  Where the 9-32-row
- * GEMV or the 33-160-row band kernel splits K across workgroups, its fp32 partials go
+ * arguments, kernels and results as sc_qmm_bf16, bit for bit.  Where the 9-160-row
+ * band kernel or the 9-32-row GEMV splits K across workgroups, its fp32 partials go
  * to a file-scope device array of SC_QMM_NOALLOC_SCRATCH_BYTES (one per GPU, held
  * until the process ends) instead of the library's growable buffer.  A shape whose
  * partials (splits * M * N floats) exceed it runs on the next kernel that needs no
@@ -197,9 +198,9 @@ int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
  * xn = RMSNorm(x + residual) when norm_weight_or_null is given (xn_out and, with a
  * residual, h_out receive xn and x + residual as for sc_qmm_rmsnorm_bf16).  The
  * decode GEMV (M <= 8) pairs gate row i with up row I + i inside one tile and writes
- * act [M, I] directly; at 9-32 rows (split-K GEMV) and 33-160 rows (band kernel, K a
- * multiple of 512) the split-K pass rounds gate and up to bf16 (bias after rounding)
- * and writes act [M, I]; above that the GEMM pairs gate and up columns in its tiles
+ * act [M, I] directly; at 9-160 rows (band kernel, K a multiple of 512, chosen by
+ * shape up to 32 rows; else the split-K GEMV) the split-K pass rounds gate and up to bf16 (bias after
+ * rounding) and writes act [M, I]; above that the GEMM pairs gate and up columns in its tiles
  * and writes act itself (I a multiple of 16).  gate_up_scratch [M, 2I] is required but
  * used only where none of these applies: then the product goes there and the
  * standalone sc_silu_mul_bf16 follows (the same values).  Outputs must not overlap

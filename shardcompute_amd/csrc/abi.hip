@@ -156,21 +156,33 @@ static int check_qmm(const void *x, const void *wq, const void *s, const void *b
     return SC_OK;
 }
 
+// Whether the automatic choice is the band kernel: 33-160 rows (measured faster than
+// the GEMM's 256-row tiles up to 128 rows, slower at 256), and 9-32 rows where the
+// 16-column GEMV's K splits or x staging cost more than the band's stream: K above
+// 4096 or at most 8192 weight rows (measured on the decode shapes: 8B down at 16
+// rows 17 against 25 us, the 70B shard's q|k|v, gate|up and down at 32 rows 10, 19, 13
+// against 11, 23, 15 us; 8B gate|up at 16 rows 29 against 24 us stays on the GEMV).
+static bool band_first(int64_t M, int64_t N, int64_t K) {
+    if (M > 32) return M <= 160;
+    return M > 8 && (K > 4096 || N <= 8192);
+}
+
 static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
                         int group_size, void *stream, int path, bool no_alloc = false) {
     int rc = check_qmm(x, wq, s, b, y, M, N, K, bits, group_size);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    // 33-160 rows: the band kernel (measured faster than the GEMM's 256-row tiles up to
-    // 128 rows, slower at 256)
-    if (path == SC_QMM_PATH_AUTO) path = M <= 32 ? SC_QMM_PATH_GEMV : M <= 160 ? SC_QMM_PATH_BAND : SC_QMM_PATH_GEMM;
+    if (path == SC_QMM_PATH_AUTO) path = band_first(M, N, K) ? SC_QMM_PATH_BAND : M <= 32 ? SC_QMM_PATH_GEMV
+                                                                                    : SC_QMM_PATH_GEMM;
     if (path == SC_QMM_PATH_BAND) {
-        // 33-256 rows (or any M <= 256 when asked for): the weight-streaming band kernel;
-        // shapes it does not take (K not a multiple of 512) go to the GEMM
+        // any M <= 256: the weight-streaming band kernel; shapes it does not take (K not
+        // a multiple of 512, partials beyond the no-alloc scratch) go to the GEMVs up to
+        // 32 rows, to the GEMM above
         rc = launch_qgemm_band(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, 0, 0);
         if (rc != SC_EUNSUPPORTED) return rc;
-        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        if (M > 32) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        path = SC_QMM_PATH_GEMV;
     }
     if (path == SC_QMM_PATH_GEMV) {
         // M <= 8: persistent LDS-DMA GEMV; otherwise (or when x does not fit its
@@ -255,15 +267,15 @@ static int qmm_fused(const uint16_t *x, const uint16_t *res, const uint16_t *nw,
         if (rc) return rc;
     }
     if (!swiglu_half) return qmm_dispatch(xin, wq, s, b, bias, y, M, N, K, bits, group_size, stream, SC_QMM_PATH_AUTO);
-    if (M > 8 && M <= 32) {
-        // the 9-32-row GEMV's split-K pass applies silu(gate) * up itself
-        rc = launch_qgemv16(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half);
-        if (rc != SC_EUNSUPPORTED) return rc;
-    }
-    if (M > 32 && M <= 160) {
+    if (band_first(M, N, K)) {
         // the band kernel's split-K pass applies silu(gate) * up itself
         rc = launch_qgemm_band(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half, 0,
                                0);
+        if (rc != SC_EUNSUPPORTED) return rc;
+    }
+    if (M > 8 && M <= 32) {
+        // the 9-32-row GEMV's split-K pass applies silu(gate) * up itself
+        rc = launch_qgemv16(xin, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, false, (int)swiglu_half);
         if (rc != SC_EUNSUPPORTED) return rc;
     }
     if (M > 32) {

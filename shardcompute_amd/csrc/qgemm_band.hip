@@ -27,10 +27,13 @@
 //   Every stage's DMA list has the same length per producer, so each producer waits
 //   for its part of stage g with one vmcnt immediate; the barrier then publishes the
 //   stage and frees the slots the previous stage read.
-// * Dequant in registers: bf16(s q + b), one fp32 FMA per weight (the GEMM's rule).
-//   The k order inside a group is permuted so that a lane's codes of the 4 MFMA k-steps
-//   are one 16-byte LDS read (W4): lane half h, step ks holds k = 32 h + 8 ks + e; x
-//   rows use the same order (16-byte chunk 4 h + ks).
+// * Dequant in registers.  Above 32 rows: bf16(s q + b), one fp32 FMA per weight (the
+//   GEMM's rule).  Up to 32 rows (one x block): the decode GEMVs' rule, exact codes on
+//   MFMA and the group's scale and bias applied to its fp32 sums (s P + b S), so that
+//   a decode batch rounds as a single sequence does.  The k order inside a group is
+//   permuted so that a lane's codes of the 4 MFMA k-steps are one 16-byte LDS read
+//   (W4): lane half h, step ks holds k = 32 h + 8 ks + e; x rows use the same order
+//   (16-byte chunk 4 h + ks).
 // * Rows are XOR-swizzled in 16-byte chunks (x by row, codes by row / 2), so the
 //   operand reads are free of LDS bank conflicts; the DMA writes lanes in order, so
 //   each lane loads the chunk that belongs at its position.
@@ -189,6 +192,9 @@ __global__ void __launch_bounds__(64 * (NW + NP)) qgemm_band_kernel(BandArgs a) 
     const int rr = 32 * wave + li;                     // this lane's weight row in the tile
     uint32_t nib = 0x0F0F0F0Fu;                        // opaque: one v_cvt_f32_ubyteN per code
     asm volatile("" : "+s"(nib));
+    uint32_t nib16 = 0x000F000Fu, magic = 0x43004300u; // opaque: one v_and_or_b32 per code pair
+    asm volatile("" : "+s"(nib16));
+    asm volatile("" : "+v"(magic));
     f32x16_t acc[MT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[i] = f32x16_t{};
@@ -210,6 +216,39 @@ __global__ void __launch_bounds__(64 * (NW + NP)) qgemm_band_kernel(BandArgs a) 
         } else {               // group gi = chunks 4 gi .. 4 gi + 3; this lane's two
             wv0 = *reinterpret_cast<const uint4 *>(ws + 16 * ((4 * gi + 2 * h) ^ wsw));
             wv1 = *reinterpret_cast<const uint4 *>(ws + 16 * ((4 * gi + 2 * h + 1) ^ wsw));
+        }
+        if constexpr (MT == 1) {
+            // Up to 32 rows: the decode GEMVs' rule (qgemv_m1_kernel, qgemv16_kernel),
+            // so a batch computes as one sequence does: the MFMAs take the exact codes
+            // (W4: 128 + q in bf16, slots [q0 q4 q1 q5 q2 q6 q3 q7], x permuted alike;
+            // W8: q), a second MFMA chain with all-ones weights sums the group's x, and
+            // y += s * P + (b - 128 s) * S (W8: b * S) in fp32.
+            const uint32_t ones = 0x3F803F80u;
+            const bf16x8_t B1 = as_bf16x8(ones, ones, ones, ones);
+            f32x16_t P = f32x16_t{}, S = f32x16_t{};
+            uint4 xn = *reinterpret_cast<const uint4 *>(xs + xoff(0, 0));
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                uint4 xv = xn;
+                if (ks + 1 < 4) xn = *reinterpret_cast<const uint4 *>(xs + xoff(0, ks + 1));
+                bf16x8_t B;
+                if (BITS == 4) {
+                    xv = perm_w4x(xv);
+                    const uint32_t w = wc(wv0, ks);
+                    B = as_bf16x8(and_or(w, nib16, magic), and_or(w >> 4, nib16, magic),
+                                  and_or(w >> 8, nib16, magic), and_or(w >> 12, nib16, magic));
+                } else {
+                    const uint4 v = ks < 2 ? wv0 : wv1;
+                    const uint32_t w0 = wc(v, 2 * (ks & 1)), w1 = wc(v, 2 * (ks & 1) + 1);
+                    B = as_bf16x8(byte_pair_lo(w0), byte_pair_hi(w0), byte_pair_lo(w1), byte_pair_hi(w1));
+                }
+                P = mfma32x32x16(as_bf16x8(xv), B, P);
+                S = mfma32x32x16(as_bf16x8(xv), B1, S);
+            }
+            const float cf = BITS == 4 ? fmaf(-128.f, sf, bf) : bf;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[0][r] = fmaf(sf, P[r], fmaf(cf, S[r], acc[0][r]));
+            return;
         }
         // x operands one k-step ahead of the MFMAs that use them
         uint4 xa[2][MT];
@@ -340,11 +379,13 @@ int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
     const int P = di.num_cus;
 
     // Plan: 8-wave workgroups (256 rows) unless too few tiles would be left to fill the
-    // CUs even with every scale/bias block a split of its own; then the K splits that
-    // bring the workgroups to about one round (two per CU for the small 4-wave ones).
+    // CUs even with every scale/bias block a split of its own (twice over above 32 rows,
+    // three quarters over up to 32: measured on the decode shapes); then the K splits
+    // that bring the workgroups to about one round (two per CU for the small 4-wave
+    // ones).
     int nw = force_nw ? force_nw : 8;
     if (nw != 4 && nw != 8) return set_error(SC_EINVAL, "qgemm_band: waves %d (4 or 8)", nw);
-    if (!force_nw && (long)((N + 255) / 256) * nb < 2L * P) nw = 4;
+    if (!force_nw && (long)((N + 255) / 256) * nb < (mt == 1 ? 3L * P / 4 : 2L * P)) nw = 4;
     if (mt > 2) nw = 4;
     const int tiles = (N + 32 * nw - 1) / (32 * nw);
     const int per_cu = band_lds(bits, mt, nw) <= 80 * 1024 ? 2 : 1;
