@@ -40,15 +40,28 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
     const int nv = D >> 3;
     const uint4 *xr = reinterpret_cast<const uint4 *>(x + (size_t)row * D);
     const uint4 *rr = res ? reinterpret_cast<const uint4 *>(res + (size_t)row * D) : nullptr;
-    uint4 hv[NORM_MAXV];
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+    // every load of the row (and of the weight) is issued before the first use: the
+    // loads of a thread's chunks are independent, and one round trip to memory is
+    // the kernel's main cost at decode sizes
+    uint4 hv[NORM_MAXV], rv[NORM_MAXV], wv[NORM_MAXV];
+#pragma unroll
+    for (int i = 0; i < NORM_MAXV; ++i) {
+        const int idx = threadIdx.x + i * NORM_THREADS;
+        if (idx < nv) {
+            hv[i] = xr[idx];
+            if (rr) rv[i] = rr[idx];
+            wv[i] = wr[idx];
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NORM_MAXV; ++i) {
         const int idx = threadIdx.x + i * NORM_THREADS;
         if (idx < nv) {
-            uint4 v = xr[idx];
+            uint4 v = hv[i];
             if (rr) {
-                v = add_bf16x8(v, rr[idx]);
+                v = add_bf16x8(v, rv[i]);
                 if (h_out) reinterpret_cast<uint4 *>(h_out + (size_t)row * D)[idx] = v;
             }
             hv[i] = v;
@@ -63,12 +76,11 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
 #pragma unroll
     for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
     const float root = rms_root(tot, D, eps);
-    const uint4 *wr = reinterpret_cast<const uint4 *>(w);
     uint4 *yr = reinterpret_cast<uint4 *>(y + (size_t)row * D);
 #pragma unroll
     for (int i = 0; i < NORM_MAXV; ++i) {
         const int idx = threadIdx.x + i * NORM_THREADS;
-        if (idx < nv) yr[idx] = norm_bf16x8(hv[i], wr[idx], root);
+        if (idx < nv) yr[idx] = norm_bf16x8(hv[i], wv[i], root);
     }
 }
 
@@ -430,6 +442,15 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     const int T = a.cache_len[0] + a.S;
     const int used = min(a.nsplit, (T + a.kps - 1) / a.kps);   // <= 64 by construction
     const float *pp = a.part + wid * a.nsplit * (D + 4);
+    constexpr int PER = D / 64;
+    // the first PF partials' values are loaded with the (m, l) pairs, in one round trip
+    // (past `used` they repeat the last stored partial and are not added)
+    constexpr int PF = 8;
+    float vf[PF][PER];
+#pragma unroll
+    for (int k = 0; k < PF; ++k)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) vf[k][e] = pp[(size_t)min(k, used - 1) * (D + 4) + lane + 64 * e];
     const float mi = lane < used ? pp[(size_t)lane * (D + 4) + D] : -INFINITY;
     const float li = lane < used ? pp[(size_t)lane * (D + 4) + D + 1] : 0.f;
     float M = mi;
@@ -437,9 +458,16 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
     const float wi = (mi == -INFINITY) ? 0.f : exp2f(mi - M);
     const float L = wave_sum(wi * li);
-    constexpr int PER = D / 64;
     float acc[PER] = {};
-    int i = 0;
+#pragma unroll
+    for (int k = 0; k < PF; ++k) {
+        const float wk = __shfl(wi, k);
+        if (k < used) {
+#pragma unroll
+            for (int e = 0; e < PER; ++e) acc[e] += wk * vf[k][e];
+        }
+    }
+    int i = PF;
     for (; i + 4 <= used; i += 4) {
         float v[4][PER];
 #pragma unroll
