@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 11
+#define SC_ABI_VERSION 12
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV or band kernel (by shape); 33-160:
@@ -148,6 +148,25 @@ int sc_dequantize_bf16(const uint32_t *wq, const uint16_t *scales, const uint16_
  */
 int sc_quantize_affine(const float *w, int64_t rows, int64_t K, int bits, int group_size, uint32_t *wq,
                        uint16_t *scales, uint16_t *biases, void *hip_stream);
+
+/*
+ * The projection that feeds a residual add and the next RMSNorm:
+ *   y = qmm(x) (+ bias after rounding), h = bf16(y + residual), xn = RMSNorm(h) * w.
+ * h_out [M, N] receives h and xn_out [M, N] xn (N a multiple of 8 up to 16384;
+ * residual, norm_weight, h_out, xn_out and the bias 16-byte aligned; h_out and xn_out
+ * overlap neither each other nor the inputs).  Where the product splits K (the
+ * 9-160-row kernels) the norm's pass sums the partials itself, one launch in place
+ * of the split-K pass and the norm; otherwise the product writes y into xn_out and
+ * the pass reads it there.  Bit for bit sc_qmm_bf16 followed by sc_rms_norm_bf16
+ * with that residual.  Replaces o_proj / down_proj with the residual add and the
+ * next layernorm when the all-reduce between them is the identity
+ * (src/shardcompute/parallel/transformer.py:246 then 250, and 252 then the next
+ * layer's 239; quantized_linear.py:435-443 at world_size 1).
+ */
+int sc_qmm_add_rmsnorm_bf16(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                            const uint16_t *bias_or_null, const uint16_t *residual, const uint16_t *norm_weight,
+                            float eps, uint16_t *h_out, uint16_t *xn_out, int64_t M, int64_t N, int64_t K, int bits,
+                            int group_size, void *hip_stream);
 
 /*
  * y = qmm(xn) with xn = RMSNorm(x + residual) (residual optional): the

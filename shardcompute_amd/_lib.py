@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_BAND = 0, 1, 2, 3
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -30,6 +30,7 @@ EXPORTS = (
     "sc_dequantize_bf16",
     "sc_quantize_affine",
     "sc_qmm_rmsnorm_bf16",
+    "sc_qmm_add_rmsnorm_bf16",
     "sc_decode_head_bf16",
     "sc_qmm_swiglu_bf16",
     "sc_rms_norm_bf16",
@@ -98,6 +99,8 @@ def load():
         f32 = ctypes.c_float
         lib.sc_qmm_rmsnorm_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p]
         lib.sc_qmm_rmsnorm_bf16.restype = i32
+        lib.sc_qmm_add_rmsnorm_bf16.argtypes = [p, p, p, p, p, p, p, f32, p, p, i64, i64, i64, i32, i32, p]
+        lib.sc_qmm_add_rmsnorm_bf16.restype = i32
         lib.sc_decode_head_bf16.argtypes = [p, p, p, f32, p, p, p, p, p, p, p, i64, i64, i64, i32, i32, p, p, i64,
                                             i64, p, p, i64, p, i64, p]
         lib.sc_decode_head_bf16.restype = i32
@@ -291,6 +294,35 @@ def qmm_rmsnorm(x, norm_weight, eps, wq, scales, biases, residual=None, h_out=No
                                  group_size, _stream(x))
     _check(rc, "sc_qmm_rmsnorm_bf16")
     return y.reshape(*lead, N), xn.reshape(*lead, K)
+
+
+def qmm_add_rmsnorm(x, wq, scales, biases, residual, norm_weight, eps, bias=None, bits=4, group_size=64,
+                    h_out=None, xn_out=None):
+    """y = qmm(x) (+ bias), then h = y + residual and xn = RMSNorm(h): the projection
+    before a residual add and the next norm, its split-K pass folded into the norm.
+    Returns (h, xn), both [*lead, N]; bit for bit ``qmm`` then ``rms_norm(y,
+    residual=residual)``.  Outputs must be distinct from each other and the inputs."""
+    lib = load()
+    _require_gpu(x, wq, scales, biases, residual, norm_weight, bias, h_out, xn_out)
+    K = x.shape[-1]
+    _rows(x, K, "x")
+    lead = x.shape[:-1]
+    M = x.numel() // K
+    wq, scales, biases, bias, N = _qmm_common(wq, scales, biases, bias, bits, group_size, K)
+    _rows(residual, N, "residual")
+    if residual.numel() != M * N:
+        raise ValueError(f"residual must hold {M} rows of {N}")
+    if norm_weight.shape != (N,) or norm_weight.dtype != torch.bfloat16:
+        raise ValueError(f"norm weight must be bf16 [{N}]")
+    h = h_out if h_out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    xn = xn_out if xn_out is not None else torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    _rows(h, N, "h_out")
+    _rows(xn, N, "xn_out")
+    rc = lib.sc_qmm_add_rmsnorm_bf16(_ptr(x), _ptr(wq), _ptr(scales), _ptr(biases), _ptr(bias), _ptr(residual),
+                                     _ptr(norm_weight.contiguous()), float(eps), _ptr(h), _ptr(xn), M, N, K, bits,
+                                     group_size, _stream(x))
+    _check(rc, "sc_qmm_add_rmsnorm_bf16")
+    return h.reshape(*lead, N), xn.reshape(*lead, N)
 
 
 DECODE_HEAD_WORKSPACE_BYTES = 16

@@ -17,7 +17,8 @@ int launch_qgemv_dma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, c
                      const DmaFused *fused = nullptr);
 bool qgemv_dma_eligible(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, int M, int K);
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half = 0);
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half = 0,
+                   SplitKeep *keep = nullptr);
 int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
@@ -25,7 +26,7 @@ int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
                       int swiglu_half = 0);
 int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
-                      bool no_alloc, int swiglu_half, int force_nw, int force_split);
+                      bool no_alloc, int swiglu_half, int force_nw, int force_split, SplitKeep *keep = nullptr);
 int launch_vocab_gather(const void *ids, int ids_is_int64, int64_t T, const uint16_t *table, int64_t v_local,
                         int64_t D, int64_t vocab_start, uint16_t *out, hipStream_t stream);
 int launch_qembed_gather(const void *ids, int ids_is_int64, int64_t T, const uint32_t *wq, const uint16_t *s,
@@ -36,6 +37,9 @@ int launch_quantize(const float *w, int64_t rows, int64_t K, int bits, uint32_t 
 int launch_dequantize(const uint32_t *wq, const uint16_t *s, const uint16_t *b, int64_t rows, int64_t K, int bits,
                       uint16_t *out, hipStream_t stream);
 
+int launch_split_add_rms_norm(const float *partials, int splits, const uint16_t *y_in, const uint16_t *bias,
+                              const uint16_t *res, const uint16_t *w, uint16_t *h_out, uint16_t *out, long rows, long D,
+                              float eps, hipStream_t stream);
 int launch_rms_norm(const uint16_t *x, const uint16_t *res, const uint16_t *w, uint16_t *y, uint16_t *h_out,
                     long rows, long D, float eps, hipStream_t stream);
 int launch_rope_append(uint16_t *qkv, long qkv_stride, long B, long S, long H, long Hkv, long D,
@@ -169,7 +173,7 @@ static bool band_first(int64_t M, int64_t N, int64_t K) {
 
 static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                         const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K, int bits,
-                        int group_size, void *stream, int path, bool no_alloc = false) {
+                        int group_size, void *stream, int path, bool no_alloc = false, SplitKeep *keep = nullptr) {
     int rc = check_qmm(x, wq, s, b, y, M, N, K, bits, group_size);
     if (rc) return rc;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -179,7 +183,7 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         // any M <= 256: the weight-streaming band kernel; shapes it does not take (K not
         // a multiple of 512, partials beyond the no-alloc scratch) go to the GEMVs up to
         // 32 rows, to the GEMM above
-        rc = launch_qgemm_band(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, 0, 0);
+        rc = launch_qgemm_band(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, 0, 0, keep);
         if (rc != SC_EUNSUPPORTED) return rc;
         if (M > 32) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         path = SC_QMM_PATH_GEMV;
@@ -190,7 +194,7 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         // takes the 32-column generic-K kernel; x that fits no LDS layout, the GEMM
         rc = launch_qgemv_dma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         if (rc != SC_EUNSUPPORTED) return rc;
-        rc = launch_qgemv16(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc);
+        rc = launch_qgemv16(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, keep);
         if (rc != SC_EUNSUPPORTED) return rc;
         rc = launch_qgemv_skinny(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         if (rc != SC_EUNSUPPORTED) return rc;
@@ -477,6 +481,33 @@ int sc_qmm_rmsnorm_bf16(const uint16_t *x, const uint16_t *residual_or_null, con
     if (!norm_weight || !xn_out) return set_error(SC_EINVAL, "qmm_rmsnorm: null pointer argument");
     return qmm_fused(x, residual_or_null, norm_weight, eps, h_out_or_null, xn_out, wq, scales, biases, bias_or_null, y,
                      M, N, K, bits, group_size, hip_stream, 0, nullptr);
+}
+
+int sc_qmm_add_rmsnorm_bf16(const uint16_t *x, const uint32_t *wq, const uint16_t *scales, const uint16_t *biases,
+                            const uint16_t *bias_or_null, const uint16_t *residual, const uint16_t *norm_weight,
+                            float eps, uint16_t *h_out, uint16_t *xn_out, int64_t M, int64_t N, int64_t K, int bits,
+                            int group_size, void *hip_stream) {
+    int rc = check_qmm(x, wq, scales, biases, xn_out, M, N, K, bits, group_size);
+    if (rc) return rc;
+    if (!residual || !norm_weight || !h_out) return set_error(SC_EINVAL, "qmm_add_rmsnorm: null pointer argument");
+    if (N % 8 || N > 16384) return set_error(SC_EINVAL, "qmm_add_rmsnorm: N=%lld must be a multiple of 8 up to 16384",
+                                             (long long)N);
+    if (!aligned(residual, 16) || !aligned(norm_weight, 16) || !aligned(h_out, 16) || !aligned(xn_out, 16) ||
+        !aligned(bias_or_null, 16))
+        return set_error(SC_EINVAL, "qmm_add_rmsnorm: activation, weight and bias pointers must be 16-byte aligned");
+    const size_t xb = (size_t)M * K * 2, yb = (size_t)M * N * 2;
+    if (overlap(h_out, yb, x, xb) || overlap(h_out, yb, residual, yb) || overlap(xn_out, yb, x, xb) ||
+        overlap(xn_out, yb, residual, yb) || overlap(h_out, yb, xn_out, yb))
+        return set_error(SC_EINVAL, "qmm_add_rmsnorm: h_out and xn_out must not overlap each other or the inputs");
+    // the product's split-K partials go straight into the norm's pass; a product that
+    // writes its rows itself writes them into xn_out, which the pass then reads
+    SplitKeep keep;
+    rc = qmm_dispatch(x, wq, scales, biases, bias_or_null, xn_out, M, N, K, bits, group_size, hip_stream,
+                      SC_QMM_PATH_AUTO, false, &keep);
+    if (rc) return rc;
+    return launch_split_add_rms_norm(keep.partials, keep.splits, xn_out, keep.splits ? bias_or_null : nullptr,
+                                     residual, norm_weight, h_out, xn_out, M, N, eps,
+                                     reinterpret_cast<hipStream_t>(hip_stream));
 }
 
 int sc_decode_head_bf16(const uint16_t *x, const uint16_t *residual_or_null, const uint16_t *norm_weight, float eps,

@@ -84,6 +84,85 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
     }
 }
 
+// The residual add and RMSNorm after a projection, with the projection's split-K
+// pass folded in: y = bf16(sum over splits of partials [splits, rows, D], in split
+// order) (+ bias, rounded again) -- or y read as bf16 when splits = 0 -- then
+// h = bf16(y + res) and out = RMSNorm(h) * w, bit for bit launch_qmm_finalize followed
+// by add_rms_norm_kernel (the sum of squares in that kernel's 256-thread partition).
+// One workgroup of 1024 threads per row: one chunk of 8 per thread and pass, all of a
+// chunk's loads in flight together.  y_in may be `out` (each row is read whole
+// before it is written).
+constexpr int PNORM_THREADS = 1024;
+
+__global__ void __launch_bounds__(PNORM_THREADS)
+split_add_rms_norm_kernel(const float *partials, int splits, const uint16_t *y_in, const uint16_t *bias,
+                          const uint16_t *res, const uint16_t *w, uint16_t *h_out, uint16_t *out, long rows, int D,
+                          float eps) {
+    __shared__ uint4 hs[NORM_THREADS * NORM_MAXV];
+    __shared__ float red[NORM_THREADS / 64];
+    const long row = blockIdx.x;
+    const int nv = D >> 3;
+    const size_t total = (size_t)rows * D;
+    for (int c = threadIdx.x; c < nv; c += PNORM_THREADS) {
+        const size_t e0 = (size_t)row * D + 8 * (size_t)c;
+        const uint4 r = reinterpret_cast<const uint4 *>(res + e0)[0];
+        uint4 y;
+        if (splits == 0) {
+            y = reinterpret_cast<const uint4 *>(y_in + e0)[0];
+        } else {
+            float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            int sp = 0;
+            for (; sp + 4 <= splits; sp += 4) {          // four splits' loads in flight
+                float4 p[4][2];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const float4 *src = reinterpret_cast<const float4 *>(partials + (size_t)(sp + u) * total + e0);
+                    p[u][0] = src[0];
+                    p[u][1] = src[1];
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    v[0] += p[u][0].x; v[1] += p[u][0].y; v[2] += p[u][0].z; v[3] += p[u][0].w;
+                    v[4] += p[u][1].x; v[5] += p[u][1].y; v[6] += p[u][1].z; v[7] += p[u][1].w;
+                }
+            }
+            for (; sp < splits; ++sp) {
+                const float4 *src = reinterpret_cast<const float4 *>(partials + (size_t)sp * total + e0);
+                const float4 p0 = src[0], p1 = src[1];
+                v[0] += p0.x; v[1] += p0.y; v[2] += p0.z; v[3] += p0.w;
+                v[4] += p1.x; v[5] += p1.y; v[6] += p1.z; v[7] += p1.w;
+            }
+            uint32_t o[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = f2bf(v[e]);
+            if (bias) {
+                const uint4 bb = reinterpret_cast<const uint4 *>(bias)[c];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e] = f2bf(bf2f(o[e]) + bfe(bb, e));
+            }
+            y = make_uint4(o[0] | (o[1] << 16), o[2] | (o[3] << 16), o[4] | (o[5] << 16), o[6] | (o[7] << 16));
+        }
+        const uint4 h = add_bf16x8(y, r);
+        reinterpret_cast<uint4 *>(h_out + e0)[0] = h;
+        hs[c] = h;
+    }
+    __syncthreads();
+    if (threadIdx.x < NORM_THREADS) {
+        float ss = 0.f;
+        for (int c = threadIdx.x; c < nv; c += NORM_THREADS) ss = sumsq_bf16x8(ss, hs[c]);
+        ss = wave_sum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    }
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
+    const float root = rms_root(tot, D, eps);
+    for (int c = threadIdx.x; c < nv; c += PNORM_THREADS)
+        reinterpret_cast<uint4 *>(out + (size_t)row * D)[c] =
+            norm_bf16x8(hs[c], reinterpret_cast<const uint4 *>(w)[c], root);
+}
+
 // ---------------------------------------------------------------- RoPE + KV append
 //
 // Token (b, s) goes to cache slot cache_len + s and is rotated for position
@@ -916,6 +995,25 @@ int launch_rms_norm(const uint16_t *x, const uint16_t *res, const uint16_t *w, u
     if (rows == 0) return SC_OK;
     hipLaunchKernelGGL(add_rms_norm_kernel, dim3((unsigned)rows), dim3(NORM_THREADS), 0, stream, x, res, w, y,
                        h_out, (int)D, eps);
+    SC_HIP_CHECK(hipGetLastError());
+    return SC_OK;
+}
+
+int launch_split_add_rms_norm(const float *partials, int splits, const uint16_t *y_in, const uint16_t *bias,
+                              const uint16_t *res, const uint16_t *w, uint16_t *h_out, uint16_t *out, long rows, long D,
+                              float eps, hipStream_t stream) {
+    if ((splits > 0 ? !partials : !y_in) || !res || !w || !h_out || !out)
+        return set_error(SC_EINVAL, "add_rms_norm: null pointer");
+    if (rows < 0 || D <= 0 || D % 8 || D > (long)NORM_THREADS * NORM_MAXV * 8)
+        return set_error(SC_EINVAL, "add_rms_norm: D=%ld must be a positive multiple of 8 up to %d", D,
+                         NORM_THREADS * NORM_MAXV * 8);
+    if (((uintptr_t)partials | (uintptr_t)y_in | (uintptr_t)res | (uintptr_t)w | (uintptr_t)h_out |
+         (uintptr_t)out | (uintptr_t)bias) % 16)
+        return set_error(SC_EINVAL, "add_rms_norm: pointers must be 16-byte aligned");
+    if (rows == 0) return SC_OK;
+    if (rows > 0x7FFFFFFFL) return set_error(SC_EINVAL, "add_rms_norm: too many rows");
+    hipLaunchKernelGGL(split_add_rms_norm_kernel, dim3((unsigned)rows), dim3(PNORM_THREADS), 0, stream, partials,
+                       splits, y_in, bias, res, w, h_out, out, rows, (int)D, eps);
     SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
 }

@@ -362,9 +362,11 @@ static int band_lds(int bits, int mt, int nw) {
 // need more are SC_EUNSUPPORTED) instead of the library-owned buffer.
 // swiglu_half > 0: the weight is gate|up stacked (N = 2 swiglu_half) and y
 // [M, swiglu_half] receives silu(gate) * up, applied by the split-K pass.
+// keep (plain products): the partials are left to the caller's pass (keep->splits > 0)
+// instead of being summed into y.
 int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
-                      bool no_alloc, int swiglu_half, int force_nw, int force_split) {
+                      bool no_alloc, int swiglu_half, int force_nw, int force_split, SplitKeep *keep) {
     if (M < 1 || M > 256 || N < 1) return SC_EUNSUPPORTED;
     if (bits != 4 && bits != 8) return SC_EUNSUPPORTED;
     if (K % 512) return SC_EUNSUPPORTED;                 // whole 8-group scale/bias blocks
@@ -426,6 +428,11 @@ int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
                      : launch_band_mt<8, 8>(a, nw, tiles, ksplit, stream);
     }
     if (rc) return rc;
+    if (keep) {
+        keep->partials = with_partials ? a.partials : nullptr;
+        keep->splits = with_partials ? ksplit : 0;
+        if (with_partials && !swiglu_half) return SC_OK;
+    }
     if (with_partials) return launch_qmm_finalize(a.partials, ksplit, M, N, bias, y, swiglu_half, stream);
     return SC_OK;
 }

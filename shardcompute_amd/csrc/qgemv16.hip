@@ -485,8 +485,11 @@ static int launch_gemv16_t(const Gemv16Args &a, const Gemv16Plan &p, hipStream_t
 // need more than it holds are rejected) instead of the library-owned buffer.
 // swiglu_half > 0: the weight is gate|up stacked (N = 2 swiglu_half) and y [M, swiglu_half]
 // receives silu(gate) * up, applied by the partials' pass (which then always runs).
+// keep (plain products): the partials are left to the caller's pass (keep->splits > 0)
+// instead of being summed into y.
 int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b, const uint16_t *bias,
-                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half) {
+                   uint16_t *y, int M, int N, int K, int bits, hipStream_t stream, bool no_alloc, int swiglu_half,
+                   SplitKeep *keep) {
     if (M < 1 || M > 32) return SC_EUNSUPPORTED;
     if (swiglu_half && (swiglu_half < 0 || N != 2 * swiglu_half)) return SC_EUNSUPPORTED;
     if (((uintptr_t)s % 16) || ((uintptr_t)b % 16)) return SC_EUNSUPPORTED;
@@ -523,6 +526,11 @@ int launch_qgemv16(const uint16_t *x, const uint32_t *wq, const uint16_t *s, con
     return set_error(SC_EUNSUPPORTED, "qgemv16: bits=%d", bits);
 #undef SC_G16
     if (rc) return rc;
+    if (keep) {
+        keep->partials = with_partials ? a.partials : nullptr;
+        keep->splits = with_partials ? p.splits : 0;
+        if (with_partials && !swiglu_half) return SC_OK;
+    }
     if (with_partials) return launch_qmm_finalize(a.partials, p.splits, M, N, bias, y, swiglu_half, stream);
     return SC_OK;
 }

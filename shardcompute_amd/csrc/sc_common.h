@@ -251,6 +251,14 @@ int splitk_scratch(size_t partial_floats, size_t n_counters, SplitKScratch *out)
 // array of SC_QMM_NOALLOC_SCRATCH_BYTES (address looked up once per device).
 int qmm_noalloc_scratch(float **out);
 
+// A split-K product whose caller runs its own pass over the fp32 partials
+// [splits, M, N] instead of launch_qmm_finalize; splits = 0 when the product wrote y
+// itself (one split).
+struct SplitKeep {
+    const float *partials = nullptr;
+    int splits = 0;
+};
+
 // y = bf16(sum over splits of partials [splits, M, N] in split order) (+ bias after
 // rounding); with half > 0 the product is gate|up stacked (N = 2 half) and y [M, half]
 // receives silu(gate) * up of the rounded values.

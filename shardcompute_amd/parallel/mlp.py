@@ -103,6 +103,13 @@ class ParallelMLP:
         xn = norm(h, residual=residual, h_out=h_out, out=xn_out)
         return self.intermediate(xn, gu_out=gu_out, out=act_out)
 
+    def act_from_xn(self, xn, act_out=None, gu_out=None):
+        """The activation of the input projections of an already normalised input
+        (the gated SiLU applied inside the gate|up product)."""
+        if self.fused_swiglu:
+            return self.gate_up.swiglu_call(xn, None, act_out=act_out, gu_out=gu_out)
+        return self.intermediate(xn, gu_out=gu_out, out=act_out)
+
     async def down_from_gate_up(self, gate_up, act_out=None):
         """down(f(gate) * up) from the fused gate|up product (gated MLPs)."""
         if not self.use_gated:

@@ -224,6 +224,25 @@ class QuantizedRowParallelLinear:
             raise RuntimeError("Weight not loaded")
         return self._qmm(x)
 
+    @property
+    def folds_norm(self) -> bool:
+        """Whether forward_add_norm runs as one fused call: the all-reduce between the
+        product and the residual add is the identity."""
+        return self.communicator is None or isinstance(self.communicator, IdentityCommunicator)
+
+    def forward_add_norm(self, x, residual, norm, h_out=None, xn_out=None):
+        """(h, xn) = (forward(x) + residual, norm(h)) for a bias-free RMSNorm, the
+        product's split-K pass folded into the norm's (one launch fewer; the same
+        bits as forward followed by the norm).  Only with an identity all-reduce."""
+        if self.quantized_weight is None:
+            raise RuntimeError("Weight not loaded")
+        if not self.folds_norm or not norm.fusable:
+            raise ValueError("forward_add_norm needs an identity all-reduce and a bias-free norm")
+        norm._check()
+        return _lib.qmm_add_rmsnorm(x, self.quantized_weight, self.scales, self.biases_quant, residual, norm.weight,
+                                    norm.eps, bias=self.bias if self.has_bias else None, bits=self.bits,
+                                    group_size=self.group_size, h_out=h_out, xn_out=xn_out)
+
     def add_bias(self, x: torch.Tensor) -> torch.Tensor:
         if self.has_bias and self.bias is not None:
             return (x.float() + self.bias.float()).to(x.dtype)

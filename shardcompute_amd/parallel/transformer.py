@@ -36,7 +36,7 @@ from .attention import ParallelAttention
 from .column_linear import ColumnParallelLinear
 from .embedding import ParallelEmbedding, QuantizedParallelEmbedding, VocabParallelEmbedding
 from .mlp import ParallelMLP
-from .quantized_linear import QuantizedColumnParallelLinear
+from .quantized_linear import QuantizedColumnParallelLinear, QuantizedRowParallelLinear
 from ._tensors import default_device, to_device
 
 logger = logging.getLogger(__name__)
@@ -300,29 +300,59 @@ class ParallelTransformer:
         additive attention mask every layer's attention adds to its scores).
 
         Each RMSNorm (with the residual add before it) runs inside the projection
-        that reads it, and the SiLU gate inside down_proj.  The residual stream
+        that reads it, or, above 8 rows, inside the projection that feeds the
+        residual add (o_proj and down_proj, their split-K pass folded into the
+        norm's), and the SiLU gate inside the gate|up product.  The residual stream
         alternates between two buffers (a kernel's h_out may not alias its input).
         Returns (h, the last layer's MLP output whose residual add is pending)."""
         h_alt = bufs.h2 if bufs is not None else torch.empty_like(h)
+        xn_buf = bufs.xn if bufs is not None else None
         pending = None
+        xn_next = None          # the next layer's normalised input, when down_proj computed it
+        L = len(self.layers)
         for i, layer in enumerate(self.layers):
             att, mlp = layer.attention, layer.mlp
-            qkv, _ = att.qkv.norm_call(h, layer.input_layernorm, residual=pending,
-                                       h_out=h_alt if pending is not None else None,
-                                       xn_out=bufs.xn if bufs is not None else None,
-                                       out=bufs.qkv if bufs is not None else None)
-            if pending is not None:
-                h, h_alt = h_alt, h
+            if xn_next is not None:
+                qkv = att.qkv(xn_next, out=bufs.qkv if bufs is not None else None)
+            else:
+                qkv, _ = att.qkv.norm_call(h, layer.input_layernorm, residual=pending,
+                                           h_out=h_alt if pending is not None else None, xn_out=xn_buf,
+                                           out=bufs.qkv if bufs is not None else None)
+                if pending is not None:
+                    h, h_alt = h_alt, h
             a = att.attend_qkv(qkv, B, S, cache[i], out=bufs.attn if bufs else None,
                                workspace=bufs.workspace if bufs else None, mask=mask)
-            o = await att.o_proj.forward(a)
-            act = mlp.act_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt,
-                               xn_out=bufs.xn if bufs is not None else None,
-                               act_out=bufs.act if bufs is not None else None,
-                               gu_out=bufs.gu if bufs is not None else None)
+            act_out = bufs.act if bufs is not None else None
+            gu_out = bufs.gu if bufs is not None else None
+            if self._folds(att.o_proj, layer.post_attention_layernorm, B * S):
+                # o_proj, the residual add and the post-attention norm in one call: its
+                # split-K pass runs inside the norm's
+                _, xn = att.o_proj.forward_add_norm(a, h, layer.post_attention_layernorm, h_out=h_alt, xn_out=xn_buf)
+                act = mlp.act_from_xn(xn, act_out=act_out, gu_out=gu_out)
+            else:
+                o = await att.o_proj.forward(a)
+                act = mlp.act_call(h, layer.post_attention_layernorm, residual=o, h_out=h_alt, xn_out=xn_buf,
+                                   act_out=act_out, gu_out=gu_out)
             h, h_alt = h_alt, h
-            pending = await mlp.down_proj.forward(act)
+            xn_next = None
+            if i + 1 < L and self._folds(mlp.down_proj, self.layers[i + 1].input_layernorm, B * S):
+                # down_proj, the residual add and the next layer's input norm in one call
+                h_new, xn_next = mlp.down_proj.forward_add_norm(act, h, self.layers[i + 1].input_layernorm,
+                                                                h_out=h_alt, xn_out=xn_buf)
+                h, h_alt = h_new, h
+                pending = None
+            else:
+                pending = await mlp.down_proj.forward(act)
         return h, pending
+
+    @staticmethod
+    def _folds(proj, norm, rows: int) -> bool:
+        """Whether a row-parallel projection runs with its residual add and the next
+        norm folded in (sc_qmm_add_rmsnorm_bf16): a quantized projection with an
+        identity all-reduce, a bias-free norm, and more than 8 rows (up to 8 the
+        decode GEMV applies the norm while staging the next product's input, which
+        is one launch fewer still)."""
+        return (rows > 8 and isinstance(proj, QuantizedRowParallelLinear) and proj.folds_norm and norm.fusable)
 
     async def _head(self, h, pending, B, S, last_only, hn_out=None):
         """Final RMSNorm (of h + pending, when a residual add is pending) and lm_head."""

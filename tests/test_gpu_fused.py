@@ -161,3 +161,57 @@ def test_fused_rejects_aliasing(device):
         _lib.qmm_rmsnorm(x, nw, 1e-5, *W, residual=r, h_out=x)
     with pytest.raises(RuntimeError, match="overlap"):
         _lib.qmm_rmsnorm(x, nw, 1e-5, *W, residual=r, xn_out=r)
+
+
+@pytest.mark.parametrize("M,N,K,bits,with_bias", [(1, 4096, 4096, 4, False), (8, 4096, 14336, 4, True),
+                                                  (16, 4096, 4096, 4, False), (16, 4096, 14336, 4, True),
+                                                  (32, 8192, 1024, 4, False), (32, 8192, 3584, 8, True),
+                                                  (24, 2048, 5632, 4, False), (64, 4096, 4096, 4, True),
+                                                  (300, 2048, 2048, 8, False), (12, 16384, 1024, 4, False)])
+def test_qmm_add_rmsnorm_matches_unfused(device, M, N, K, bits, with_bias):
+    """The projection before a residual add and RMSNorm (o_proj, down_proj) with its
+    split-K pass folded into the norm's: h and xn bit for bit the plain product (its
+    own split-K pass, bias after rounding) followed by the standalone norm with that
+    residual, on every kernel the product takes (decode GEMV, band kernel with and
+    without K splits, GEMM); xn against the oracle."""
+    rng = np.random.default_rng(M * 13 + N + K + bits)
+    wq, s, b = _weights(rng, N, K, bits)
+    x, r = _bf(rng, (M, K)), _bf(rng, (M, N), 4.0)
+    nw = f32_to_bf16((1 + 0.1 * rng.standard_normal(N)).astype(np.float32))
+    bias = _bf(rng, (N,), 0.5) if with_bias else None
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd, rd, nwd = dev_bf16(x), dev_bf16(r), dev_bf16(nw)
+    bd = dev_bf16(bias) if with_bias else None
+    print(f"qmm_add_rmsnorm M={M} N={N} K={K} W{bits} bias={with_bias}", flush=True)
+    h, xn = _lib.qmm_add_rmsnorm(xd, *W, rd, nwd, 1e-5, bias=bd, bits=bits)
+    y = _lib.qmm(xd, *W, bias=bd, bits=bits)
+    h2 = torch.empty_like(y)
+    xn2 = _lib.rms_norm(y, nwd, 1e-5, residual=rd, h_out=h2)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(xn, xn2)
+    # the same buffers again (every output element rewritten; nothing carried over)
+    h.fill_(0)
+    xn.fill_(0)
+    _lib.qmm_add_rmsnorm(xd, *W, rd, nwd, 1e-5, bias=bd, bits=bits, h_out=h, xn_out=xn)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h2) and torch.equal(xn, xn2)
+    ref = quantized_matmul_f64(x, wq, s, b, 64, bits)
+    yr = bf16_to_f32(f32_to_bf16(ref.astype(np.float32)))
+    if with_bias:
+        yr = bf16_to_f32(f32_to_bf16(yr + bf16_to_f32(bias)[None]))
+    hr = f32_to_bf16(yr + bf16_to_f32(r))
+    xnr = rms_norm(bf16_to_f32(hr), nw, 1e-5)
+    assert max_abs_rel(host_u16(xn), xnr) <= LINEAR_TOL
+
+
+def test_qmm_add_rmsnorm_rejects_overlap(device):
+    rng = np.random.default_rng(5)
+    wq, s, b = _weights(rng, 1024, 1024, 4)
+    W = (dev_u32(wq), dev_bf16(s), dev_bf16(b))
+    xd, rd = dev_bf16(_bf(rng, (16, 1024))), dev_bf16(_bf(rng, (16, 1024)))
+    nwd = dev_bf16(f32_to_bf16(np.ones(1024, np.float32)))
+    with pytest.raises(RuntimeError, match="overlap"):
+        _lib.qmm_add_rmsnorm(xd, *W, rd, nwd, 1e-5, h_out=rd)
+    with pytest.raises(RuntimeError, match="overlap"):
+        out = torch.empty_like(rd)
+        _lib.qmm_add_rmsnorm(xd, *W, rd, nwd, 1e-5, h_out=out, xn_out=out)
