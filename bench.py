@@ -12,7 +12,7 @@ Printed (one JSON line on stdout):
 * ``value``: decode tokens/s (batch x steps / wall time of the timed steps,
   bracketed by device synchronisation);
 * ``roofline``: the dominant kernel of a decode step.  At batch 1 that is the
-  whole-trunk launch ``decode_step_kernel<4>`` (embedding and every layer in one
+  whole-trunk launch ``decode_step_kernel<4, 128, 4>`` (embedding and every layer in one
   persistent kernel; the step adds the final RMSNorm + lm_head GEMV, which also
   selects the greedy token):
   algorithmic bytes per launch (every layer's packed weights + bf16 scales and
@@ -94,6 +94,11 @@ def parse_args():
     p.add_argument("--attn-only", action="store_true",
                    help="run only the prefill attention of the Llama-3-8B heads at --prefill positions "
                         "(random q, k, v; for counter profiling)")
+    p.add_argument("--batched-decode-only", action="store_true",
+                   help="only the batched decode workloads: Llama-3-8B at batch 16 and the 70B rank-0 shard at "
+                        "batch 32, W4 (one JSON line)")
+    p.add_argument("--shard-head-only", action="store_true",
+                   help="only the vocab-sharded embedding gather and the M=64 quantized lm_head (one JSON line)")
     p.add_argument("--sweep-only", action="store_true",
                    help="only the standalone quantized-linear sweep (every (K, N), M, W4/W8), JSON on stdout")
     p.add_argument("--gemv16-only", action="store_true",
@@ -831,6 +836,16 @@ def main():
     if args.sweep_only:
         print(json.dumps(bench_qmm_sweep()), flush=True)
         return
+    if args.batched_decode_only:
+        out = {"batch16_llama3_8b_w4": bench_decode_config("Llama-3-8B W4 bs16", LLAMA3_8B, 4, 16, 2048, K),
+               "llama3_70b_rank0_of_8_w4_bs32": bench_decode_config("70B rank-0 shard W4 bs32", LLAMA3_70B, 4, 32,
+                                                                    1024, K, world_size=8)}
+        print(json.dumps(out), flush=True)
+        return
+    if args.shard_head_only:
+        print(json.dumps({"vocab_gather_config3": bench_vocab_gather(),
+                          "lm_head_m64_config3": bench_lm_head_m64(args.kernel_reps)}), flush=True)
+        return
     capacity = P + W + K + 8
     t_build = time.perf_counter()
     model = build_model(cfg, args.layers, args.bits, capacity)
@@ -935,10 +950,12 @@ def main():
              "avg_launch_us": round(g["avg_us"], 3), "bytes_per_launch": round(g["bytes_per_launch"]),
              "launches_per_step": g["launches_per_step"]}
     if trunk is not None:
+        hd = cfg["hidden"] // cfg["heads"]
         roof = {"bound": "hbm", "achieved": round(trunk["GBs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(trunk["GBs"] / HBM_PEAK_GBS, 4),
                 "traffic": traffic_of(TRUNK_TRAFFIC_FILE) if args.bits == 4 and args.layers == 32 else None,
-                "kernel": f"decode_step_kernel<{args.bits}>", "avg_launch_us": round(trunk["avg_us"], 2),
+                "kernel": f"decode_step_kernel<{args.bits}, {hd}, {4 if hd == 128 else 8}>",
+                "avg_launch_us": round(trunk["avg_us"], 2),
                 "bytes_per_launch": int(trunk["bytes"]), "launches_per_step": 1}
     else:
         roof = qroof

@@ -89,9 +89,9 @@ add_rms_norm_kernel(const uint16_t *__restrict__ x, const uint16_t *__restrict__
 // order) (+ bias, rounded again) -- or y read as bf16 when splits = 0 -- then
 // h = bf16(y + res) and out = RMSNorm(h) * w, bit for bit launch_qmm_finalize followed
 // by add_rms_norm_kernel (the sum of squares in that kernel's 256-thread partition).
-// One workgroup of 1024 threads per row: one chunk of 8 per thread and pass, all of a
-// chunk's loads in flight together.  y_in may be `out` (each row is read whole
-// before it is written).
+// One workgroup per row, one thread per chunk of 8 up to 1024 threads (256 at least):
+// all of a chunk's loads in flight together.  y_in may be `out` (each row is read
+// whole before it is written).
 constexpr int PNORM_THREADS = 1024;
 
 __global__ void __launch_bounds__(PNORM_THREADS)
@@ -103,7 +103,8 @@ split_add_rms_norm_kernel(const float *partials, int splits, const uint16_t *y_i
     const long row = blockIdx.x;
     const int nv = D >> 3;
     const size_t total = (size_t)rows * D;
-    for (int c = threadIdx.x; c < nv; c += PNORM_THREADS) {
+    const int nt = blockDim.x;
+    for (int c = threadIdx.x; c < nv; c += nt) {
         const size_t e0 = (size_t)row * D + 8 * (size_t)c;
         const uint4 r = reinterpret_cast<const uint4 *>(res + e0)[0];
         uint4 y;
@@ -158,7 +159,7 @@ split_add_rms_norm_kernel(const float *partials, int splits, const uint16_t *y_i
 #pragma unroll
     for (int i = 0; i < NORM_THREADS / 64; ++i) tot += red[i];
     const float root = rms_root(tot, D, eps);
-    for (int c = threadIdx.x; c < nv; c += PNORM_THREADS)
+    for (int c = threadIdx.x; c < nv; c += nt)
         reinterpret_cast<uint4 *>(out + (size_t)row * D)[c] =
             norm_bf16x8(hs[c], reinterpret_cast<const uint4 *>(w)[c], root);
 }
@@ -1012,7 +1013,9 @@ int launch_split_add_rms_norm(const float *partials, int splits, const uint16_t 
         return set_error(SC_EINVAL, "add_rms_norm: pointers must be 16-byte aligned");
     if (rows == 0) return SC_OK;
     if (rows > 0x7FFFFFFFL) return set_error(SC_EINVAL, "add_rms_norm: too many rows");
-    hipLaunchKernelGGL(split_add_rms_norm_kernel, dim3((unsigned)rows), dim3(PNORM_THREADS), 0, stream, partials,
+    const int nv = (int)(D / 8);
+    const int threads = nv >= PNORM_THREADS ? PNORM_THREADS : nv <= NORM_THREADS ? NORM_THREADS : (nv + 63) / 64 * 64;
+    hipLaunchKernelGGL(split_add_rms_norm_kernel, dim3((unsigned)rows), dim3(threads), 0, stream, partials,
                        splits, y_in, bias, res, w, h_out, out, rows, (int)D, eps);
     SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
