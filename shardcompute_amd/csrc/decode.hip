@@ -258,10 +258,10 @@ v_append_kernel(const uint16_t *__restrict__ qkv, long qkv_stride, int S, int H,
 //   S^T[32 keys x 16 cols] = K[keys, D] . Q^T       (2 x D/32 MFMA 16x16x32)
 //   online softmax down each column (fp32, exp2 domain)
 //   O^T[D x 16 cols]      += Vt[D, keys] . P^T      (D/16 MFMA 16x16x32)
-// With S^T in the D layout (lane = column, 4 keys per lane-group and tile) the
-// probabilities already sit where operand B of the second product wants them:
-// key slot 8g + r <-> key 4g + r (tile 0) and 8g + 4 + r <-> key 16 + 4g + r
-// (tile 1); Vt is read in the same key order, so no LDS round trip is needed.
+// With S^T in the D layout (lane = column, 4 keys per lane-group and tile) and the
+// block's keys permuted into its rows (attn_load), lane group g holds keys
+// 8g .. 8g + 7 in order: exactly the k slots of operand B of the second product,
+// and Vt is read for the same keys, so no LDS round trip is needed.
 // The probabilities enter the second product as bf16 (as in flash attention).
 // Keys may be split over waves (decode); partial (m, l, O) then go to a
 // workspace and attn_combine_kernel merges them.
@@ -288,26 +288,30 @@ constexpr int ATTN_STRIDE = ATTN_WAVES * ATTN_KB;  // a workgroup's waves take i
 
 // One key block's operands, loaded together: K rows for S^T (two 16-key tiles x
 // D/32 k-steps) and Vt rows for O^T (D/16 tiles x keys {4g..4g+3, 16+4g..16+4g+3}).
+// A block's keys are permuted on the way into S^T so that lane group g ends up with
+// the 8 consecutive keys kb + 8g .. kb + 8g + 7 (tile 0 row r = key 8 (r / 4) + r % 4,
+// tile 1 row r = key 8 (r / 4) + 4 + r % 4): the probabilities are then operand B of
+// O^T in natural key order, and each lane's V^T operand is one 16-byte load of 8
+// consecutive cached keys (a V^T row's 64 bytes of the block in one instruction's
+// 4 lanes, rather than 32-byte halves in two).
 template <int D>
 struct AttnBlock {
     uint4 k[2][D / 32];
-    uint2 v[D / 16][2];
+    uint4 v[D / 16];
 };
 
 template <int D>
 __device__ __forceinline__ void attn_load(AttnBlock<D> &blk, const uint16_t *kbase, const uint16_t *vbase, int T_cap,
                                           int kb, int c, int g) {
+    const int k0 = kb + 8 * (c >> 2) + (c & 3);
 #pragma unroll
     for (int u = 0; u < D / 32; ++u) {
-        blk.k[0][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + c) * D + 32 * u + 8 * g);
-        blk.k[1][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)(kb + 16 + c) * D + 32 * u + 8 * g);
+        blk.k[0][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)k0 * D + 32 * u + 8 * g);
+        blk.k[1][u] = *reinterpret_cast<const uint4 *>(kbase + (size_t)(k0 + 4) * D + 32 * u + 8 * g);
     }
 #pragma unroll
-    for (int n = 0; n < D / 16; ++n) {
-        const uint16_t *vr = vbase + (size_t)(16 * n + c) * T_cap + kb + 4 * g;
-        blk.v[n][0] = *reinterpret_cast<const uint2 *>(vr);
-        blk.v[n][1] = *reinterpret_cast<const uint2 *>(vr + 16);
-    }
+    for (int n = 0; n < D / 16; ++n)
+        blk.v[n] = *reinterpret_cast<const uint4 *>(vbase + (size_t)(16 * n + c) * T_cap + kb + 8 * g);
 }
 
 // S^T, masked online softmax and O^T update for one block of 32 keys.  Cache slots
@@ -325,11 +329,12 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(blk.k[0][u]), qv[u], s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(blk.k[1][u]), qv[u], s1, 0, 0, 0);
     }
+    // sv[j]: key kb + 8 g + j
     float sv[8];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        sv[r] = (kb + 4 * g + r <= limit) ? s0[r] * scale_log2 : -INFINITY;
-        sv[4 + r] = (kb + 16 + 4 * g + r <= limit) ? s1[r] * scale_log2 : -INFINITY;
+        sv[r] = (kb + 8 * g + r <= limit) ? s0[r] * scale_log2 : -INFINITY;
+        sv[4 + r] = (kb + 8 * g + 4 + r <= limit) ? s1[r] * scale_log2 : -INFINITY;
     }
     if (MASKED) {
         // The scores are in log2 units, so the mask is scaled by log2(e).  A finite mask
@@ -341,7 +346,7 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
         constexpr float LOG2E = 1.4426950408889634f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            const int key = kb + 16 * (r >> 2) + 4 * g + (r & 3);
+            const int key = kb + 8 * g + r;
             if (key <= limit) {
                 const float mv = mrow[(long)key * mst];
                 sv[r] += (mv == -INFINITY) ? -INFINITY : fmaxf(mv * LOG2E, -FLT_MAX);
@@ -365,12 +370,12 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
     m = mn;
     const bf16x8_t pb8 = as_bf16x8(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]), pack_bf16x2(p[4], p[5]),
                                    pack_bf16x2(p[6], p[7]));
-    // keys kb + 4g + 0..3 (piece 0) and kb + 16 + 4g + 0..3 (piece 1)
+    // word i of a lane's V^T piece: keys kb + 8g + 2i, + 1
     uint32_t mk[4] = {0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu};
     if (kb + ATTN_KB > vend) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int k = kb + 16 * (i >> 1) + 4 * g + 2 * (i & 1);
+            const int k = kb + 8 * g + 2 * i;
             mk[i] = (k < vend ? 0xFFFFu : 0u) | (k + 1 < vend ? 0xFFFF0000u : 0u);
         }
     }
@@ -380,8 +385,8 @@ __device__ __forceinline__ void attn_block(const AttnBlock<D> &blk, const bf16x8
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[r] *= alpha;
         o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            as_bf16x8(blk.v[n][0].x & mk[0], blk.v[n][0].y & mk[1], blk.v[n][1].x & mk[2], blk.v[n][1].y & mk[3]),
-            pb8, acc, 0, 0, 0);
+            as_bf16x8(blk.v[n].x & mk[0], blk.v[n].y & mk[1], blk.v[n].z & mk[2], blk.v[n].w & mk[3]), pb8, acc,
+            0, 0, 0);
     }
 }
 
