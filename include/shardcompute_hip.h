@@ -14,7 +14,8 @@
  *    -2 unsupported configuration, -3 HIP runtime error); sc_last_error() then
  *    holds a message (thread-local, valid until the next failing call).
  *  - The kernels allocate nothing per call.  The split-K path of sc_qmm_bf16 (and of
- *    the products inside sc_qmm_rmsnorm_bf16 / sc_qmm_swiglu_bf16 at 9-160 rows) uses a
+ *    the products inside sc_qmm_rmsnorm_bf16 / sc_qmm_swiglu_bf16 / sc_qmm_add_rmsnorm_bf16:
+ *    9-160 rows, and larger products whose 256-wide tiles fill at most half the GPU) uses a
  *    library-owned scratch per device, allocated on first need and grown (with a
  *    device synchronisation) when a larger shape arrives: calls that overlap on one
  *    device (concurrent streams) race on it, and the first call of a new largest

@@ -23,7 +23,7 @@ int launch_qgemv_skinny(const uint16_t *x, const uint32_t *wq, const uint16_t *s
                         const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream);
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
-                      int swiglu_half = 0);
+                      int swiglu_half = 0, bool no_alloc = false);
 int launch_qgemm_band(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits, hipStream_t stream,
                       bool no_alloc, int swiglu_half, int force_nw, int force_split, SplitKeep *keep = nullptr);
@@ -185,7 +185,7 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         // 32 rows, to the GEMM above
         rc = launch_qgemm_band(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, no_alloc, 0, 0, 0, keep);
         if (rc != SC_EUNSUPPORTED) return rc;
-        if (M > 32) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        if (M > 32) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, 0, no_alloc);
         path = SC_QMM_PATH_GEMV;
     }
     if (path == SC_QMM_PATH_GEMV) {
@@ -198,9 +198,10 @@ static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s
         if (rc != SC_EUNSUPPORTED) return rc;
         rc = launch_qgemv_skinny(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
         if (rc != SC_EUNSUPPORTED) return rc;
-        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, 0, no_alloc);
     }
-    if (path == SC_QMM_PATH_GEMM) return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st);
+    if (path == SC_QMM_PATH_GEMM)
+        return launch_qgemm_mfma(x, wq, s, b, bias, y, (int)M, (int)N, (int)K, bits, st, 0, no_alloc);
     return set_error(SC_EINVAL, "qmm: unknown path %d", path);
 }
 

@@ -22,6 +22,7 @@
 //   rounding (the reference adds it to the bf16 matmul result,
 //   quantized_linear.py:179-180).
 #include "sc_common.h"
+#include "../../include/shardcompute_hip.h"
 
 namespace sc {
 
@@ -41,6 +42,10 @@ struct GemmArgs {
     // ic = (n_base + c) / 32 * 16 + u % 16; y receives act [M, I] = silu(gate) * up.
     // (The pointers are not offset for a column range; n_base locates it.)
     int swiglu_i, n_base;
+    // Split K (grid y = splits): split z takes groups [z gps, z gps + gps) and writes
+    // fp32 partials [splits, M, N] (plain products only); gps >= G: no split, y is bf16.
+    float *partials;
+    int gps;
 };
 
 namespace {
@@ -89,7 +94,9 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 2, wn = wave & 3;
-    const int M = a.M, N = a.N, K = a.K, G = a.G;
+    const int M = a.M, N = a.N, K = a.K;
+    const int g0 = (int)blockIdx.y * a.gps;              // this split's first group
+    const int G = min(a.G - g0, a.gps);                  // and its stages
 
     // XCD-aware tile order: workgroup w runs on XCD w % 8; XCD x takes the tiles
     // [x * per, (x + 1) * per) of the m-major order, so its workgroups share x rows
@@ -102,10 +109,11 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
     // ---- x tile: thread -> chunk (tid & 7) of rows (tid >> 3) + 64 i, i < 4, 16 B each
     // (named registers rather than an array, so that they stay out of scratch)
     const int xr_ = tid >> 3, xc_ = tid & 7;
-    const uint16_t *xs0 = a.x + (size_t)min(m0 + xr_, M - 1) * K + xc_ * 8;
-    const uint16_t *xs1 = a.x + (size_t)min(m0 + xr_ + 64, M - 1) * K + xc_ * 8;
-    const uint16_t *xs2 = a.x + (size_t)min(m0 + xr_ + 128, M - 1) * K + xc_ * 8;
-    const uint16_t *xs3 = a.x + (size_t)min(m0 + xr_ + 192, M - 1) * K + xc_ * 8;
+    const uint16_t *xk = a.x + (size_t)g0 * BK;
+    const uint16_t *xs0 = xk + (size_t)min(m0 + xr_, M - 1) * K + xc_ * 8;
+    const uint16_t *xs1 = xk + (size_t)min(m0 + xr_ + 64, M - 1) * K + xc_ * 8;
+    const uint16_t *xs2 = xk + (size_t)min(m0 + xr_ + 128, M - 1) * K + xc_ * 8;
+    const uint16_t *xs3 = xk + (size_t)min(m0 + xr_ + 192, M - 1) * K + xc_ * 8;
     const uint32_t xd = swz(xr_, xc_);      // rows + 64 i land at + 64 * 128 * i (same swizzle)
     uint4 xv0, xv1, xv2, xv3;
     auto load_x = [&](int g) {
@@ -132,9 +140,9 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
         wrow = u < 16 ? ic : a.swiglu_i + ic;
     }
     const uint8_t *wsrc = reinterpret_cast<const uint8_t *>(a.wq) + (size_t)wrow * ((size_t)K * BITS / 8) +
-                          wp * (CPT * BITS / 8);
-    const uint16_t *ssrc = a.s + (size_t)wrow * G;
-    const uint16_t *bsrc = a.b + (size_t)wrow * G;
+                          (size_t)g0 * (BK * BITS / 8) + wp * (CPT * BITS / 8);
+    const uint16_t *ssrc = a.s + (size_t)wrow * a.G + g0;
+    const uint16_t *bsrc = a.b + (size_t)wrow * a.G + g0;
     auto load_w = [&](int g, WRegs<BITS, CPT> &r) {
         const uint8_t *p = wsrc + (size_t)g * (BK * BITS / 8);
         if (NW == 4) {
@@ -338,6 +346,24 @@ __global__ void __launch_bounds__(THREADS) qgemm_mfma_kernel(GemmArgs a) {
             }
         }
     };
+    if (a.partials) {
+        // split K: this split's fp32 sums, natural column order, no bias (the split-K
+        // pass sums the splits in order, then rounds and adds it)
+        float *pz = a.partials + (size_t)blockIdx.y * M * N;
+#pragma unroll
+        for (int j = 0; j < Gm::NJ; ++j) {
+            const int n = n0 + wn * Gm::WN + j * 32 + li;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = mw + i * 32 + 8 * (r >> 2) + (r & 3);
+                    if (m < M) pz[(size_t)m * N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
     if (a.swiglu_i) {
         if (m0 + BM <= M) store_swiglu(std::false_type{});
         else store_swiglu(std::true_type{});
@@ -374,13 +400,14 @@ static int launch_qgemm_cols(const GemmArgs &full, int n0, int Nc, hipStream_t s
                                          hipFuncAttributeMaxDynamicSharedMemorySize, Geo<BN>::LDS));
         configured = true;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(THREADS), Geo<BN>::LDS, stream, a);
+    const int splits = a.partials ? (a.G + a.gps - 1) / a.gps : 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)splits), dim3(THREADS), Geo<BN>::LDS, stream, a);
     SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
 }
 
 template <int BITS>
-static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream) {
+static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream, bool no_alloc) {
     // The tile width with the shorter estimated time: waves of tiles over the CUs times
     // the cost of one tile, a 128-wide tile costing 0.64 of a 256-wide one (measured
     // on the Llama-3-8B shapes at M = 2048: it reads more LDS per MFMA).  One partial
@@ -388,6 +415,37 @@ static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream) {
     const int cus = device_info().num_cus;
     const int N = a.N, mt = a.mt;
     const long tiles256 = (long)mt * ((N + 255) / 256);
+    // Wide tiles filling at most a quarter of the CUs, over K >= 4096 (a few hundred
+    // rows of x): split K so that the tiles times the splits make about one round, each
+    // split at least 8 groups; the fp32 partials go through the split-K pass (which
+    // applies SwiGLU for a gate|up product, whose columns then stay in their natural
+    // order).  Measured on the sweep shapes: at 512 rows, 14336 -> 4096 207 -> 96 us and
+    // 5632 -> 2048 84 -> 39 us; with more tiles, or K of 2048, the partials' traffic
+    // cost more than the idle CUs (512 x 4096 -> 14336: 91 -> 104 us split in two).
+    if (4 * tiles256 <= cus && a.G >= 64) {
+        int ks = (int)(cus / tiles256);
+        if (ks > a.G / 8) ks = a.G / 8;
+        const int gps = (a.G + ks - 1) / ks;
+        ks = (a.G + gps - 1) / gps;
+        const size_t need = (size_t)ks * a.M * N;
+        // without allocation: the allocation-free scratch when the partials fit, else K whole
+        if (ks >= 2 && (!no_alloc || need * sizeof(float) <= (size_t)SC_QMM_NOALLOC_SCRATCH_BYTES)) {
+            SplitKScratch ws;
+            const int rc = no_alloc ? qmm_noalloc_scratch(&ws.partials) : splitk_scratch(need, 1, &ws);
+            if (rc) return rc;
+            GemmArgs p = a;
+            const int half = a.swiglu_i;
+            p.swiglu_i = 0;
+            p.n_base = 0;
+            p.bias = nullptr;
+            p.ldy = N;
+            p.partials = ws.partials;
+            p.gps = gps;
+            const int rc2 = launch_qgemm_cols<BITS, 256>(p, 0, N, stream);
+            if (rc2) return rc2;
+            return launch_qmm_finalize(ws.partials, ks, a.M, N, a.bias, a.y, half, stream);
+        }
+    }
     const long waves256 = (tiles256 + cus - 1) / cus;
     const long waves128 = ((long)mt * ((N + 127) / 128) + cus - 1) / cus;
     if (!(100 * waves256 <= 64 * waves128)) return launch_qgemm_cols<BITS, 128>(a, 0, N, stream);
@@ -405,10 +463,11 @@ static int launch_qgemm_t(const GemmArgs &a, hipStream_t stream) {
 }
 
 // swiglu_half = I > 0: the weight stacks gate and up (N = 2I, I a multiple of 16) and y
-// receives act [M, I] = silu(gate) * up (row stride I).
+// receives act [M, I] = silu(gate) * up (row stride I).  no_alloc: split-K partials only
+// in the allocation-free scratch, K kept whole where they do not fit.
 int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
                       const uint16_t *bias, uint16_t *y, int M, int N, int K, int bits,
-                      hipStream_t stream, int swiglu_half) {
+                      hipStream_t stream, int swiglu_half, bool no_alloc) {
     if (bits != 4 && bits != 8) return set_error(SC_EUNSUPPORTED, "qgemm: bits=%d", bits);
     if (swiglu_half && (swiglu_half % 16 || N != 2 * swiglu_half)) return SC_EUNSUPPORTED;
     if (K % BK) return set_error(SC_EINVAL, "qgemm: K=%d not a multiple of %d", K, BK);
@@ -422,7 +481,9 @@ int launch_qgemm_mfma(const uint16_t *x, const uint32_t *wq, const uint16_t *s, 
     a.n_base = 0;
     a.mt = (M + BM - 1) / BM;
     a.nt = a.tiles = 0;
-    return bits == 4 ? launch_qgemm_t<4>(a, stream) : launch_qgemm_t<8>(a, stream);
+    a.partials = nullptr;
+    a.gps = a.G;
+    return bits == 4 ? launch_qgemm_t<4>(a, stream, no_alloc) : launch_qgemm_t<8>(a, stream, no_alloc);
 }
 
 }  // namespace sc
