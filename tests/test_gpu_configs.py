@@ -49,12 +49,15 @@ LOGIT_TOL = 3e-2
 # within 0.0095 of the oracle.  A wiring or indexing error gives O(1) differences.
 DEEP_LOGIT_TOL = 6e-2        # 22 layers, against the oracle
 PATH_TOL_32 = 8e-2           # 32 layers, between kernel paths
-# 80 layers, batch 32 against batch 1 (the 9-32-row GEMV against the batch-1 GEMV at
-# every projection, the attention split differently): measured over 128 decode steps
-# at positions 1024-1151, W4 and W8, max-abs-rel 0.068-0.113 and rms-relative
-# 0.073-0.091, flat in the position (no growth from step 1 to step 127).
+# 80 layers, batch 32 against batch 1 (the 32-row kernels against the batch-1 GEMV at
+# every projection, the attention split differently, and the prefill's q|k|v at
+# 1024 rows with K split against whole K at 32768): measured over 128 decode steps at
+# positions 1024-1151, W4 and W8, max-abs-rel 0.07-0.11 and rms-relative 0.07-0.11,
+# flat in the position (no growth from step 1 to step 127).  The floor is set by the
+# depth: the prefill's logits alone (step 0) move by 0.087 rms-relative when only the
+# order of layer 0's q|k|v fp32 sums changes (K split in two at 1024 rows).
 PATH_TOL_80 = 1.5e-1
-PATH_RMS_80 = 1e-1
+PATH_RMS_80 = 1.5e-1
 
 def run(coro):
     return asyncio.run(coro)
