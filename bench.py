@@ -535,6 +535,19 @@ def bench_lm_head_m64(reps=10):
             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "TFLOPs": round(tf, 1)}
 
 
+def qmm_kernel_label(M, N, K, cus=256):
+    """The kernel sc_qmm_bf16's automatic path takes for an M x K -> N product (the
+    choice csrc/abi.hip and csrc/qgemm.hip make, restated for the sweep's labels)."""
+    band = K % 512 == 0 and (M <= 160 if M > 32 else K >= 4096 if M == 8 else
+                             M > 8 and (K > 4096 or N <= 8192))
+    if band:
+        return "band"
+    if M <= 32:
+        return "gemv"
+    tiles256 = ((M + 255) // 256) * ((N + 255) // 256)
+    return "gemm, K split" if 4 * tiles256 <= cus and K // 64 >= 64 else "gemm"
+
+
 SWEEP_KN = [(2048, 2560), (2048, 5632), (5632, 2048), (4096, 6144), (4096, 14336), (14336, 4096)]
 SWEEP_M = [1, 8, 32, 512, 2048]
 
@@ -592,7 +605,7 @@ def bench_qmm_sweep(reps=5):
                 us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
                 nbytes = qmm_bytes(M, N, K, bits)
                 flops = 2.0 * M * N * K
-                kernel = ("gemv" if M <= 32 else "band" if M <= 160 and K % 512 == 0 else "gemm")
+                kernel = qmm_kernel_label(M, N, K)
                 row = {"bits": bits, "M": M, "K": K, "N": N, "kernel": kernel, "gpu_us": round(us, 2)}
                 if M <= 32:
                     gbs = nbytes / (us * 1e-6) / 1e9
