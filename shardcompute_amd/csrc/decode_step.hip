@@ -50,6 +50,9 @@ namespace step {
 
 using namespace dma;
 
+// rows of the stacked q|k|v projection
+constexpr int qkv_rows(int H, int Hkv, int D) { return (H + 2 * Hkv) * D; }
+
 constexpr int WORKERS = 8;
 constexpr int CTL = WORKERS;                // the control wave
 constexpr int THREADS = 64 * (WORKERS + 1);
@@ -683,59 +686,72 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     const uint2 *src = a.buf[B_PART];
                     const bool act = lane < a.NR;
                     const size_t wb = ((size_t)(kvh * a.NR + min(lane, a.NR - 1)) * a.R + hr) * (D + 2);
-                    // word pairs: pair 0 = (m, l); pair i >= 1 = O values d0 + 2 (i - 1), + 1
-                    uint32_t pend = act ? ((2u << (C / 2)) - 1u) : 0u;
+                    // word pairs: pair 0 = (m, l); pair i >= 1 = O values d0 + 2 (i - 1), + 1.
+                    // Values go in batches of 16 (C up to 32): the first batch is polled
+                    // with (m, l), each batch is merged and published before the next is
+                    // read, so only one batch is held in registers.
                     float mv = -INFINITY, lv = 0.f, ov[16];
+                    // poll pairs [p0, p0 + n) (n <= 9) until every one carries the epoch
+                    auto poll = [&](int p0, int n) __attribute__((always_inline)) -> bool {
+                        uint32_t pend = act ? ((1u << n) - 1u) : 0u;
 #pragma unroll
-                    for (int d = 0; d < 16; ++d) ov[d] = 0.f;
-                    for (int it = 0;; ++it) {
-                        unsigned long long v[18];
+                        for (int d = 0; d < 16; ++d) ov[d] = 0.f;
+                        for (int it = 0;; ++it) {
+                            unsigned long long v[18];
 #pragma unroll
-                        for (int i = 0; i < 9; ++i) {
-                            const uint2 *p = src + wb + (i == 0 ? D : d0 + 2 * (i - 1));
-                            if (i <= C / 2) {
-                                v[2 * i] = ll_load(p);
-                                v[2 * i + 1] = ll_load(p + 1);
-                            } else {
-                                v[2 * i] = v[2 * i + 1] = 0ull;
-                            }
-                        }
-#pragma unroll
-                        for (int i = 0; i < 9; ++i) {
-                            if ((pend & (1u << i)) && (uint32_t)(v[2 * i] >> 32) == ep_in &&
-                                (uint32_t)(v[2 * i + 1] >> 32) == ep_in) {
-                                const float f0 = __uint_as_float((uint32_t)v[2 * i]);
-                                const float f1 = __uint_as_float((uint32_t)v[2 * i + 1]);
-                                if (i == 0) {
-                                    mv = f0;
-                                    lv = f1;
+                            for (int i = 0; i < 9; ++i) {
+                                const int pi = p0 + i;
+                                const uint2 *p = src + wb + (pi == 0 ? D : d0 + 2 * (pi - 1));
+                                if (i < n) {
+                                    v[2 * i] = ll_load(p);
+                                    v[2 * i + 1] = ll_load(p + 1);
                                 } else {
-                                    ov[2 * (i - 1)] = f0;
-                                    ov[2 * (i - 1) + 1] = f1;
+                                    v[2 * i] = v[2 * i + 1] = 0ull;
                                 }
-                                pend &= ~(1u << i);
                             }
+#pragma unroll
+                            for (int i = 0; i < 9; ++i) {
+                                if ((pend & (1u << i)) && (uint32_t)(v[2 * i] >> 32) == ep_in &&
+                                    (uint32_t)(v[2 * i + 1] >> 32) == ep_in) {
+                                    const float f0 = __uint_as_float((uint32_t)v[2 * i]);
+                                    const float f1 = __uint_as_float((uint32_t)v[2 * i + 1]);
+                                    if (p0 + i == 0) {
+                                        mv = f0;
+                                        lv = f1;
+                                    } else {
+                                        // value pair p0 + i - 1 of the batch starting at pair p0
+                                        const int q = p0 == 0 ? i - 1 : i;
+                                        ov[2 * q] = f0;
+                                        ov[2 * q + 1] = f1;
+                                    }
+                                    pend &= ~(1u << i);
+                                }
+                            }
+                            if (__ballot(pend != 0u) == 0ull) return true;
+                            if ((it & 15) == 15 && (timed_out() ||
+                                __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0))
+                                return false;
                         }
-                        if (__ballot(pend != 0u) == 0ull) break;
-                        if ((it & 15) == 15 && (timed_out() ||
-                            __hip_atomic_load(a.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)) {
-                            ok = false;
-                            break;
+                    };
+                    float wr = 0.f, inv = 0.f;
+                    for (int b0 = 0; ok && b0 < C; b0 += 16) {
+                        const int nb = min(16, C - b0);            // values in this batch
+                        ok = b0 == 0 ? poll(0, 1 + nb / 2) : poll(1 + b0 / 2, nb / 2);
+                        if (!ok) break;
+                        if (b0 == 0) {
+                            if (!act) {
+                                mv = -INFINITY;
+                                lv = 0.f;
+                            }
+                            const float M = lanes_max(mv);
+                            wr = (mv == -INFINITY) ? 0.f : exp2f(mv - M);
+                            const float L = lanes_sum(act ? wr * lv : 0.f);
+                            inv = 1.f / L;
                         }
-                    }
-                    if (ok) {
-                        if (!act) {
-                            mv = -INFINITY;
-                            lv = 0.f;
-                        }
-                        const float M = lanes_max(mv);
-                        const float wr = (mv == -INFINITY) ? 0.f : exp2f(mv - M);
-                        const float L = lanes_sum(act ? wr * lv : 0.f);
-                        const float inv = 1.f / L;
-                        float lo = 0.f, hi = 0.f;                    // lane d / 2 keeps values d, d + 1
+                        float lo = 0.f, hi = 0.f;                // lane d / 2 keeps values b0 + d, + 1
 #pragma unroll
                         for (int d = 0; d < 16; d += 2) {
-                            if (d < C) {
+                            if (d < nb) {
                                 const float s0 = lanes_sum(act ? wr * ov[d] : 0.f);
                                 const float s1 = lanes_sum(act ? wr * ov[d + 1] : 0.f);
                                 if (2 * lane == d) {
@@ -744,8 +760,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                                 }
                             }
                         }
-                        if (lane < C / 2)
-                            ll_store(a.buf[B_ATT] + c0 / 2 + lane, pack_bf16x2(lo * inv, hi * inv), epoch(jj));
+                        if (lane < nb / 2)
+                            ll_store(a.buf[B_ATT] + (c0 + b0) / 2 + lane, pack_bf16x2(lo * inv, hi * inv), epoch(jj));
                     }
                 }
             }
@@ -1164,13 +1180,22 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     int dev = 0;
     SC_HIP_CHECK(hipGetDevice(&dev));
     const DeviceInfo &di = device_info();
-    const int P = di.num_cus;
+    // Workgroups: one per CU, or one per two CUs for layers of under 32 MB of weights,
+    // whose ops are short enough that the op boundaries, not the weight stream, set
+    // the step (TinyLlama's 22 MB layers: 0.80 -> 0.75 ms per step on half the CUs;
+    // the Llama-3-8B's 109 MB layers need every CU's share of HBM).
+    const double layer_bytes = ((double)qkv_rows(H, Hkv, D) * hid + (double)hid * H * D + 2.0 * I * hid +
+                                (double)hid * I) * m->bits / 8;
+    int P = di.num_cus;
+    if (layer_bytes < 32e6 && P % 2 == 0 && (H * D) % (P / 2) == 0 && (H * D) / (P / 2) <= 32 &&
+        (P / 2) / Hkv >= 1)
+        P /= 2;
     if (P < 8 || P > 4096) return set_error(SC_EUNSUPPORTED, "decode_plan: %d CUs", P);
     const int R = H / Hkv;
     const int NR = P / Hkv;
     if (NR < 1 || NR > 64) return set_error(SC_EUNSUPPORTED, "decode_plan: %d kv heads on %d CUs", Hkv, P);
     const int C = (H * D) / P;
-    if ((H * D) % P || C < 2 || C % 2 || C > 16 || D % C)
+    if ((H * D) % P || C < 2 || C % 2 || C > 32 || D % C)
         return set_error(SC_EUNSUPPORTED, "decode_plan: attention rows do not split over %d CUs", P);
     const int qkvN = (H + 2 * Hkv) * D;
 
