@@ -10,6 +10,7 @@
 #include "sc_common.h"
 #include "dma_util.h"
 
+#include <float.h>
 #include <math.h>
 #include <type_traits>
 
@@ -65,6 +66,11 @@ struct FaArgs {
     int S, H, Hkv, R, T_cap, nqb;
     int pair_half;            // > 0: the first 2 pair_half workgroups are dispatched in heavy/light pairs
     float scale_log2;
+    // the additive mask (attn_prefill_kernel<true>): element (b, h, s, t) at
+    // mask + b msb + h msh + s mss + t mst, added to the scaled scores
+    const float *mask;
+    long msb, msh, mss, mst;
+    float mask_unscale;       // 1 / scale: a mask value in the kernel's unscaled score units
 };
 
 // exchange bits 2 and 3
@@ -82,6 +88,12 @@ __device__ __forceinline__ uint32_t fa_kswz(int r, int c) {
 // rows d and d + 8 on the same banks: 4 conflict cycles a read, measured)
 __device__ __forceinline__ uint32_t fa_vswz(int d, int c) { return (uint32_t)(d * 128 + ((c ^ ((d >> 1) & 7)) << 4)); }
 
+// ADD: the additive mask (attention.py:449-450).  Every block adds the column's mask
+// row (finite values clamped to -FLT_MAX in the kernel's units, -inf kept), loaded one
+// block ahead into registers; a column's running maximum may then stay -inf for whole
+// blocks, so probabilities of -inf scores are set to 0 explicitly, and a column whose
+// every visible score is -inf ends as 0 / 0 = NaN, as the reference's softmax does.
+template <bool ADD>
 __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -161,6 +173,27 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     for (int db = 0; db < 4; ++db) o[db] = f32x16_t{};
     float m = -INFINITY, lsum = 0.f;
 
+    // the column's mask row and the 32 values of the next block (register r of half kh:
+    // key kb + 32 kh + 16 (r / 8) + 8 lh + r % 8; keys past the column's limit read the
+    // limit's value, which the causal mask then replaces)
+    const float *mrow = nullptr;
+    float mnext[2][16];
+    auto load_mask = [&](int kb) __attribute__((always_inline)) {
+        if constexpr (ADD) {
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int t = min(kb + 32 * kh + 16 * (r >> 3) + 8 * lh + (r & 7), limit);
+                    mnext[kh][r] = mrow[(long)t * a.mst];
+                }
+        }
+    };
+    if constexpr (ADD) {
+        mrow = a.mask + (long)b * a.msb + (long)h * a.msh + (long)min(pos, last_pos) * a.mss;
+        load_mask(0);
+    }
+
     stage_blk(0, 0);
     // q's loads must be retired here, before the loop: the compiler cannot see the
     // DMA, and a wait it placed at q's first use would sit in the loop and also wait
@@ -181,6 +214,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         const uint8_t *V = K + FA_KTILE;
         // block blk + 1 goes to the stage block blk - 1 used (read before the last barrier)
         if (blk + 1 < nblk) stage_blk(kb + FA_KB, st ^ 1);
+
         // S^T for the block's two 32-key halves: register r of sacc[kh] is key
         // kb + 32 kh + 16 (r / 8) + 8 lh + r % 8
         // (the two halves' chains interleaved, so consecutive MFMAs are independent;
@@ -205,6 +239,18 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
 #pragma unroll
         for (int i = 0; i < FA_SAHEAD; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (ADD) {
+            // this block's mask (landed with the previous block's closing wait), then the
+            // next block's loads, which this block's closing wait retires
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float mv = mnext[kh][r];
+                    sacc[kh][r] += mv == -INFINITY ? -INFINITY : fmaxf(mv * a.mask_unscale, -FLT_MAX);
+                }
+            if (blk + 1 < nblk) load_mask(kb + FA_KB);
+        }
         if (MASK) {
             const int rel = limit - kb - 8 * lh;
 #pragma unroll
@@ -232,7 +278,16 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], sc, nms));
+                float p;
+                if constexpr (ADD) {
+                    // (score - m) sc: a column whose visible scores all sit at the clamp
+                    // (-FLT_MAX) gets exp2(0) for each, uniform weights; the fused form's
+                    // rounded -m sc would leave a remainder of ~1e30 there.  -inf scores
+                    // get 0 (with m = -inf, -inf - m is NaN).
+                    p = sacc[kh][r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((sacc[kh][r] - m) * sc);
+                } else {
+                    p = __builtin_amdgcn_exp2f(fmaf(sacc[kh][r], sc, nms));
+                }
                 sacc[kh][r] = p;
                 ps += p;
             }
@@ -303,7 +358,7 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
     }
     const float ltot = lsum + __shfl_xor(lsum, 32);
     if (!col_ok) return;
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    const float inv = (ADD || ltot > 0.f) ? 1.f / ltot : 0.f;
     uint16_t *orow = a.out + ((size_t)b * a.S + pos) * a.out_stride + (size_t)h * FA_D;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
@@ -323,10 +378,11 @@ __global__ void __launch_bounds__(FA_THREADS) attn_prefill_kernel(FaArgs a) {
 // columns) and returns SC_OK; returns 1, launching nothing, when it does not.  The
 // choice does not depend on the batch size, so that a sequence's result is the same
 // alone and in a batch (every column's arithmetic is its own).  The caller has
-// checked the shape, strides and pointers as launch_attention does.
+// checked the shape, strides and pointers as launch_attention does.  mask / ms: the
+// additive mask and its strides (b, h, s, t), or null.
 int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                         const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
-                        long D, float scale, hipStream_t stream) {
+                        long D, float scale, hipStream_t stream, const float *mask, const long *ms) {
     const long R = H / Hkv;
     if (D != FA_D || FA_COLS % R != 0 || ((uintptr_t)vt % 16) != 0) return 1;
     if (T_cap > (1L << 22)) return 1;    // staging offsets within one (b, kv head) slab are 32-bit
@@ -340,13 +396,18 @@ int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, co
     const long per_round = 2L * device_info().num_cus;     // two workgroups per CU (64 KB LDS each)
     f.pair_half = wgs >= per_round ? (int)(per_round / 2) : 0;
     f.scale_log2 = scale * 1.4426950408889634f;
-    static bool configured = false;
-    if (!configured) {
-        SC_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void *>(attn_prefill_kernel),
+    f.mask = mask;
+    f.msb = mask ? ms[0] : 0; f.msh = mask ? ms[1] : 0; f.mss = mask ? ms[2] : 0; f.mst = mask ? ms[3] : 0;
+    f.mask_unscale = 1.f / scale;
+    static bool configured[2] = {false, false};
+    if (!configured[mask != nullptr]) {
+        SC_HIP_CHECK(hipFuncSetAttribute(mask ? reinterpret_cast<const void *>(attn_prefill_kernel<true>)
+                                              : reinterpret_cast<const void *>(attn_prefill_kernel<false>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, FA_LDS));
-        configured = true;
+        configured[mask != nullptr] = true;
     }
-    hipLaunchKernelGGL(attn_prefill_kernel, dim3((unsigned)wgs), dim3(FA_THREADS), FA_LDS, stream, f);
+    if (mask) hipLaunchKernelGGL(attn_prefill_kernel<true>, dim3((unsigned)wgs), dim3(FA_THREADS), FA_LDS, stream, f);
+    else hipLaunchKernelGGL(attn_prefill_kernel<false>, dim3((unsigned)wgs), dim3(FA_THREADS), FA_LDS, stream, f);
     SC_HIP_CHECK(hipGetLastError());
     return SC_OK;
 }

@@ -1124,10 +1124,10 @@ int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H
 // attn_prefill.hip
 int launch_attn_prefill(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                         const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
-                        long D, float scale, hipStream_t stream);
+                        long D, float scale, hipStream_t stream, const float *mask, const long *ms);
 
 // mask (optional): the additive mask of sc_attention_masked_bf16, element (b, h, s, t)
-// at mask + b*ms[0] + h*ms[1] + s*ms[2] + t*ms[3]; a masked call runs attn_kernel.
+// at mask + b*ms[0] + h*ms[1] + s*ms[2] + t*ms[3].
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
                      long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream,
@@ -1145,9 +1145,9 @@ int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const
         return set_error(SC_EINVAL, "attention: mask strides must be given and non-negative");
     // many positions: attn_prefill_kernel (attn_prefill.hip, 128 columns a workgroup)
     // when the shape suits it; otherwise attn_kernel, which can also split the keys
-    if (!mask) {
+    {
         const int pf = launch_attn_prefill(q, q_stride, kc, vt, T_cap, cache_len, out, out_stride, B, S, H, Hkv, D,
-                                           scale, stream);
+                                           scale, stream, mask, ms);
         if (pf <= 0) return pf;
     }
     AttnPlan pl;

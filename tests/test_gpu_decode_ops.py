@@ -243,7 +243,10 @@ def _mask_for(rng, kind, B, H, S, T):
 
 
 @pytest.mark.parametrize("B,S,H,Hkv,D,past,extra,kind", [
-    (2, 64, 32, 8, 128, 0, 0, "pad"),       # a prefill the 128-column kernel would take unmasked
+    (2, 64, 32, 8, 128, 0, 0, "pad"),       # prefills: the 128-column kernel with the mask added
+    (1, 160, 32, 8, 128, 64, 32, "full"),   # a per-head mask after a cached prefix
+    (2, 96, 8, 1, 128, 0, 0, "padmin"),     # 8 q heads per kv head, left padding with finfo.min
+    (1, 64, 32, 8, 128, 0, 0, "allmin"),    # every key finfo.min: uniform weights
     (1, 48, 8, 2, 64, 100, 30, "full"),     # head_dim 64, after a cache
     (1, 1, 32, 8, 128, 2047, 256, "pad"),   # one position, keys split over workgroups
     (3, 1, 8, 1, 128, 300, 0, "full"),      # one position, 8 heads per KV head
