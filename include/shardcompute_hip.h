@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define SC_ABI_VERSION 12
+#define SC_ABI_VERSION 13
 
 /* Kernel selection for sc_qmm_bf16_path. */
 #define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV or band kernel (8-32 rows, by shape);
@@ -325,6 +325,25 @@ int sc_attention_decode_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B,
                              uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len, int64_t pos_offset,
                              float scale, uint16_t *out, int64_t out_stride, void *workspace,
                              int64_t workspace_bytes, void *hip_stream);
+
+/*
+ * sc_attention_decode_bf16 with an additive mask: every score of row b's new
+ * position, q head h and key t (the cache_len[0] + 1 keys, the new one included)
+ * gets mask[b, h, t] added after the scaling, as sc_attention_masked_bf16 adds it
+ * (element at mask + b*mask_stride_b + h*mask_stride_h + t*mask_stride_t, fp32,
+ * strides non-negative, 0 broadcasting).  Same cache contents as
+ * sc_rope_append_kv_bf16; the output equals sc_attention_masked_bf16 with S = 1
+ * within float rounding, in one launch (plus the range merge) instead of two.  A row
+ * whose visible scores are all -inf gives NaN.  Replaces ParallelAttention.forward's
+ * RoPE, KV concatenation, attention and attention_mask addition for one token
+ * (src/shardcompute/parallel/attention.py:421-466, 449-450).
+ */
+int sc_attention_decode_masked_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t H, int64_t Hkv,
+                                    int64_t D, const float *cos_t, const float *sin_t, int64_t table_len,
+                                    uint16_t *k_cache, uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len,
+                                    int64_t pos_offset, float scale, const float *mask, int64_t mask_stride_b,
+                                    int64_t mask_stride_h, int64_t mask_stride_t, uint16_t *out, int64_t out_stride,
+                                    void *workspace, int64_t workspace_bytes, void *hip_stream);
 
 /*
  * out[rows, I] = silu(gate) * up for gate_up [rows, 2I] (gate columns first), with

@@ -14,7 +14,7 @@ import torch
 
 from .build import LIB_PATH
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 PATH_AUTO, PATH_GEMV, PATH_GEMM, PATH_BAND = 0, 1, 2, 3
 
 # Exported symbols (must match include/shardcompute_hip.h).
@@ -40,6 +40,7 @@ EXPORTS = (
     "sc_attention_masked_bf16",
     "sc_attention_decode_workspace_bytes",
     "sc_attention_decode_bf16",
+    "sc_attention_decode_masked_bf16",
     "sc_silu_mul_bf16",
     "sc_act_bf16",
     "sc_add_row_bias_bf16",
@@ -122,6 +123,9 @@ def load():
         lib.sc_attention_decode_bf16.argtypes = [p, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, f32, p,
                                                  i64, p, i64, p]
         lib.sc_attention_decode_bf16.restype = i32
+        lib.sc_attention_decode_masked_bf16.argtypes = [p, i64, i64, i64, i64, i64, p, p, i64, p, p, i64, p, i64, f32,
+                                                        p, i64, i64, i64, p, i64, p, i64, p]
+        lib.sc_attention_decode_masked_bf16.restype = i32
         lib.sc_silu_mul_bf16.argtypes = [p, i64, i64, p, p]
         lib.sc_silu_mul_bf16.restype = i32
         lib.sc_act_bf16.argtypes = [p, i64, i64, i32, i32, p, p]
@@ -610,11 +614,12 @@ def attention_decode_workspace_bytes(B, H, Hkv, D, T_cap):
 
 
 def attention_decode(qkv, B, H, Hkv, D, cos_t, sin_t, k_cache, v_cache_t, cache_len, scale, pos_offset=0, out=None,
-                     workspace=None):
+                     workspace=None, mask=None, n_keys=None):
     """One decode step of attention: RoPE of row b's q and k heads (rotary position
     cache_len[0] + pos_offset), append of k and v at slot cache_len[0], and
     attention of the new position over the cache.  qkv [B, >= (H + 2Hkv) * D] is
-    not modified.  Returns out [B, H*D] bf16."""
+    not modified.  ``mask``: the reference's additive attention mask, broadcastable
+    to [B, H, 1, n_keys] (n_keys = cached positions + 1).  Returns out [B, H*D] bf16."""
     lib = load()
     _require_gpu(qkv, cos_t, sin_t, k_cache, v_cache_t, cache_len, out, workspace)
     _bf16(qkv, "qkv"), _bf16(k_cache, "k_cache"), _bf16(v_cache_t, "v_cache_t"), _i32(cache_len, "cache_len")
@@ -632,6 +637,15 @@ def attention_decode(qkv, B, H, Hkv, D, cos_t, sin_t, k_cache, v_cache_t, cache_
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=qkv.device)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if mask is not None:
+        m = broadcast_mask(mask, B, H, 1, n_keys)
+        sb, sh, _, st = m.stride()
+        rc = lib.sc_attention_decode_masked_bf16(_ptr(qkv), qkv.stride(0), B, H, Hkv, D, _ptr(cos_t), _ptr(sin_t),
+                                                 cos_t.shape[0], _ptr(k_cache), _ptr(v_cache_t), T_cap,
+                                                 _ptr(cache_len), int(pos_offset), float(scale), _ptr(m), sb, sh, st,
+                                                 _ptr(out), out.stride(0), _ptr(workspace), ws_bytes, _stream(qkv))
+        _check(rc, "sc_attention_decode_masked_bf16")
+        return out
     rc = lib.sc_attention_decode_bf16(_ptr(qkv), qkv.stride(0), B, H, Hkv, D, _ptr(cos_t), _ptr(sin_t),
                                       cos_t.shape[0], _ptr(k_cache), _ptr(v_cache_t), T_cap, _ptr(cache_len),
                                       int(pos_offset), float(scale), _ptr(out), out.stride(0), _ptr(workspace),

@@ -50,7 +50,8 @@ long attention_decode_workspace_bytes(long B, long H, long Hkv, long D, long T_c
 int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H, long Hkv, long D,
                             const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
                             long T_cap, const int32_t *cache_len, long pos_offset, float scale, uint16_t *out,
-                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream);
+                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream,
+                            const float *mask = nullptr, const long *ms = nullptr);
 int launch_attention(const uint16_t *q, long q_stride, const uint16_t *kc, const uint16_t *vt, long T_cap,
                      const int32_t *cache_len, uint16_t *out, long out_stride, long B, long S, long H, long Hkv,
                      long D, float scale, void *workspace, long workspace_bytes, hipStream_t stream,
@@ -440,6 +441,19 @@ int sc_attention_decode_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B,
     return launch_attention_decode(qkv, qkv_stride, B, H, Hkv, D, cos_t, sin_t, table_len, k_cache, v_cache_t, T_cap,
                                    cache_len, pos_offset, scale, out, out_stride, workspace, workspace_bytes,
                                    reinterpret_cast<hipStream_t>(hip_stream));
+}
+
+int sc_attention_decode_masked_bf16(const uint16_t *qkv, int64_t qkv_stride, int64_t B, int64_t H, int64_t Hkv,
+                                    int64_t D, const float *cos_t, const float *sin_t, int64_t table_len,
+                                    uint16_t *k_cache, uint16_t *v_cache_t, int64_t T_cap, const int32_t *cache_len,
+                                    int64_t pos_offset, float scale, const float *mask, int64_t mask_stride_b,
+                                    int64_t mask_stride_h, int64_t mask_stride_t, uint16_t *out, int64_t out_stride,
+                                    void *workspace, int64_t workspace_bytes, void *hip_stream) {
+    if (!mask) return set_error(SC_EINVAL, "attention_decode_masked: null mask");
+    const long ms[4] = {(long)mask_stride_b, (long)mask_stride_h, 0, (long)mask_stride_t};
+    return launch_attention_decode(qkv, qkv_stride, B, H, Hkv, D, cos_t, sin_t, table_len, k_cache, v_cache_t, T_cap,
+                                   cache_len, pos_offset, scale, out, out_stride, workspace, workspace_bytes,
+                                   reinterpret_cast<hipStream_t>(hip_stream), mask, ms);
 }
 
 int sc_silu_mul_bf16(const uint16_t *gate_up, int64_t rows, int64_t I, uint16_t *out, void *hip_stream) {

@@ -613,6 +613,8 @@ struct AttnDecArgs {
     float *part;             // [B, H, 1, nsplit, D + 4] when nsplit > 1: O[D], m, l, pad
     int H, Hkv, R, kps, nsplit;
     float scale_log2;
+    const float *mask;       // attn_decode_kernel<D, true>: additive mask, element (b, h, 0, t) at
+    long msb, msh, mst;      // mask + b msb + h msh + t mst
 };
 
 // dims [i0, i0 + 8) of the first half of a head and their partners i0 + D/2,
@@ -638,7 +640,9 @@ __device__ __forceinline__ void rope_pair8(uint4 lo, uint4 hi, const float *cv, 
     ohi = make_uint4(bb[0], bb[1], bb[2], bb[3]);
 }
 
-template <int D>
+// MASKED: the additive mask of the new position's row (attention.py:449-450), added to
+// every visible score, the new key's included, as attn_kernel<D, true> adds it.
+template <int D, bool MASKED>
 __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArgs a) {
     constexpr int U = D / 32;
     constexpr int DT = D / 16;
@@ -660,6 +664,7 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
     const int pos = a.cache_len[0];                 // slot of the new position
     const uint16_t *row = a.qkv + (size_t)b * a.qkv_stride;
     const bool col_ok = c < a.R;
+    const float *mrow = MASKED && col_ok ? a.mask + b * a.msb + (long)(hk * a.R + c) * a.msh : nullptr;
     uint4 qraw[U];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -725,17 +730,17 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
     // cached keys.  One block per wave (the usual decode split) needs no prefetch: a
     // useless one would also hold vmcnt slots that the append's stores then wait for.
     if (kb + ATTN_STRIDE >= k_hi) {
-        if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o);
+        if (kb < k_hi) attn_block<D, MASKED>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o, mrow, a.mst);
     } else {
         // the loop of attn_kernel (unconditional, clamped loads)
         while (true) {
             const int kn = kb + ATTN_STRIDE;
             attn_load<D>(nxt, kbase, vbase, a.T_cap, min(kn < k_hi ? kn : kb, clampk), c, g);
-            if (kb < k_hi) attn_block<D>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o);
+            if (kb < k_hi) attn_block<D, MASKED>(cur, qv, kb, limit, T - 1, g, a.scale_log2, m, lsum, o, mrow, a.mst);
             if (kn >= k_hi) break;
             const int kn2 = kn + ATTN_STRIDE;
             attn_load<D>(cur, kbase, vbase, a.T_cap, min(kn2 < k_hi ? kn2 : kn, clampk), c, g);
-            attn_block<D>(nxt, qv, kn, limit, T - 1, g, a.scale_log2, m, lsum, o);
+            attn_block<D, MASKED>(nxt, qv, kn, limit, T - 1, g, a.scale_log2, m, lsum, o, mrow, a.mst);
             if (kn2 >= k_hi) break;
             kb = kn2;
         }
@@ -768,7 +773,12 @@ __global__ void __launch_bounds__(64 * ATTN_WAVES) attn_decode_kernel(AttnDecArg
             for (int e = 0; e < 8; ++e) dot = fmaf(bfe(__builtin_bit_cast(uint4, qv[u]), e), bfe(kr[u], e), dot);
         dot += __shfl_xor(dot, 16);
         dot += __shfl_xor(dot, 32);
-        const float sn = col_ok ? dot * a.scale_log2 : -INFINITY;
+        float sn = col_ok ? dot * a.scale_log2 : -INFINITY;
+        if (MASKED && col_ok) {
+            // attn_block's scaling and clamp of the mask value
+            const float mv = mrow[(long)(T - 1) * a.mst];
+            sn += (mv == -INFINITY) ? -INFINITY : fmaxf(mv * 1.4426950408889634f, -FLT_MAX);
+        }
         const float mn = fmaxf(m, sn);
         const float alpha = (mn == -INFINITY) ? 1.f : exp2f(m - mn);
         const float p = (sn == -INFINITY) ? 0.f : exp2f(sn - mn);
@@ -1066,10 +1076,15 @@ long attention_decode_workspace_bytes(long B, long H, long Hkv, long D, long T_c
     return attention_workspace_bytes(B, 1, H, Hkv, D, T_cap);
 }
 
+// mask / ms (optional): the additive mask and its (b, h, s, t) strides, as for
+// launch_attention (the s stride is unused: one position per sequence)
 int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H, long Hkv, long D,
                             const float *cos_t, const float *sin_t, long table_len, uint16_t *kc, uint16_t *vt,
                             long T_cap, const int32_t *cache_len, long pos_offset, float scale, uint16_t *out,
-                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream) {
+                            long out_stride, void *workspace, long workspace_bytes, hipStream_t stream,
+                            const float *mask, const long *ms) {
+    if (mask && (!ms || ms[0] < 0 || ms[1] < 0 || ms[2] < 0 || ms[3] < 0))
+        return set_error(SC_EINVAL, "attention_decode: mask strides must be given and non-negative");
     if (!qkv || !cos_t || !sin_t || !kc || !vt || !cache_len || !out)
         return set_error(SC_EINVAL, "attention_decode: null pointer");
     if (D != 64 && D != 128) return set_error(SC_EUNSUPPORTED, "attention_decode: head_dim %ld (64 or 128 supported)", D);
@@ -1109,8 +1124,15 @@ int launch_attention_decode(const uint16_t *qkv, long qkv_stride, long B, long H
     a.kps = ca.kps; a.nsplit = ca.nsplit;
     a.scale_log2 = ca.scale_log2;
     const dim3 grid((unsigned)a.nsplit, (unsigned)Hkv, (unsigned)B);
-    if (D == 128) hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * ATTN_WAVES), 0, stream, a);
-    else hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+    a.mask = mask;
+    a.msb = mask ? ms[0] : 0; a.msh = mask ? ms[1] : 0; a.mst = mask ? ms[3] : 0;
+    if (mask) {
+        if (D == 128) hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+    } else {
+        if (D == 128) hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+        else hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, dim3(64 * ATTN_WAVES), 0, stream, a);
+    }
     SC_HIP_CHECK(hipGetLastError());
     if (ca.nsplit > 1) {
         const unsigned cb = (unsigned)((B * H + 3) / 4);

@@ -1187,9 +1187,13 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     const double layer_bytes = ((double)qkv_rows(H, Hkv, D) * hid + (double)hid * H * D + 2.0 * I * hid +
                                 (double)hid * I) * m->bits / 8;
     int P = di.num_cus;
-    if (layer_bytes < 32e6 && P % 2 == 0 && (H * D) % (P / 2) == 0 && (H * D) / (P / 2) <= 32 &&
-        (P / 2) / Hkv >= 1)
-        P /= 2;
+    // half the CUs when the merge of the attention rows still splits evenly over them
+    // (the same conditions as below, at twice the rows per workgroup)
+    auto merge_ok = [&](int p) {
+        const int c = p > 0 && (H * D) % p == 0 ? (H * D) / p : 0;
+        return c >= 2 && c % 2 == 0 && c <= 32 && D % c == 0 && p / Hkv >= 1;
+    };
+    if (layer_bytes < 32e6 && P % 2 == 0 && merge_ok(P / 2)) P /= 2;
     if (P < 8 || P > 4096) return set_error(SC_EUNSUPPORTED, "decode_plan: %d CUs", P);
     const int R = H / Hkv;
     const int NR = P / Hkv;

@@ -168,15 +168,17 @@ class ParallelAttention:
         """RoPE, cache append and attention on an already computed q|k|v product.
 
         One position per sequence (decode) runs as the fused decode attention
-        (RoPE, append and attention in one launch, plus the range merge).  ``mask``
+        (RoPE, append and attention in one launch, plus the range merge), with the
+        mask when one is given.  ``mask``
         is the reference's additive ``attention_mask``, broadcastable to
         ``[B, local heads, S, cached + S keys]`` (``attention.py:449-450``)."""
         H, Hk, D = self.local_num_heads, self.local_num_kv_heads, self.head_dim
         cos_t, sin_t = self.rope.tables(kv.cache.capacity + pos_offset, qkv.device)
-        if S == 1 and H // Hk <= 16 and mask is None:
-            return _lib.attention_decode(qkv, B, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, self.scale,
-                                         pos_offset=pos_offset, out=out, workspace=workspace)
         n_keys = kv.length + S
+        if S == 1 and H // Hk <= 16:
+            return _lib.attention_decode(qkv, B, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, self.scale,
+                                         pos_offset=pos_offset, out=out, workspace=workspace, mask=mask,
+                                         n_keys=n_keys if mask is not None else None)
         _lib.rope_append_kv(qkv, B, S, H, Hk, D, cos_t, sin_t, kv.k, kv.vt, kv.counters, pos_offset=pos_offset)
         return _lib.attention(qkv, B, S, H, Hk, D, kv.k, kv.vt, kv.counters, self.scale, out=out,
                               workspace=workspace, mask=mask, n_keys=n_keys)

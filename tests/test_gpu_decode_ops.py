@@ -487,3 +487,68 @@ def test_add_and_counters(device):
     _lib.add_i32(c, 3, n=2)
     _lib.add_i32(c[2:], -1, n=1)
     assert c.cpu().tolist() == [8, 12, 0]
+
+
+@pytest.mark.parametrize("B,H,Hkv,D,past,extra,kind", [
+    (2, 32, 8, 128, 500, 64, "pad"),        # padding keys (-inf) in a long cache: split key ranges
+    (3, 8, 1, 128, 300, 0, "full"),         # a per-head mask, 8 q heads per kv head
+    (1, 32, 4, 64, 150, 100, "full"),       # head_dim 64
+    (1, 32, 8, 128, 40, 0, "allmin"),       # every key finfo.min: uniform weights
+    (2, 32, 8, 128, 64, 0, "newonly"),      # only the new key visible (the rest -inf)
+])
+def test_attention_decode_additive_mask(device, B, H, Hkv, D, past, extra, kind):
+    """The fused decode attention with an additive mask against the oracle, the cache
+    contents against the two-kernel path's, and the output against the masked
+    two-kernel path (sc_rope_append_kv_bf16 then sc_attention_masked_bf16)."""
+    rng = np.random.default_rng(B * 5 + H + past)
+    T = past + 1
+    T_cap = ((T + extra + 31) // 32) * 32
+    rows, k, v, cos_t, sin_t = _decode_case(rng, B, H, Hkv, D, past, T_cap)
+    vt_h = np.ascontiguousarray(v.transpose(0, 1, 3, 2))
+    if kind == "newonly":
+        m = np.full((B, 1, 1, T), -np.inf, np.float32)
+        m[..., T - 1] = 0.0
+    else:
+        m = _mask_for(rng, kind, B, H, 1, T)
+    mask = torch.from_numpy(m).cuda()
+    scale = 1.0 / np.sqrt(D)
+    print(f"attention_decode with a {kind} mask {m.shape}: B={B} H={H} Hkv={Hkv} D={D} past={past}", flush=True)
+    ws = torch.empty(max(_lib.attention_decode_workspace_bytes(B, H, Hkv, D, T_cap),
+                         _lib.attention_workspace_bytes(B, 1, H, Hkv, D, T_cap), 16), dtype=torch.uint8, device="cuda")
+    kc1, vt1 = dev_bf16(k), dev_bf16(vt_h)
+    cnt1 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    out1 = _lib.attention_decode(dev_bf16(rows), B, H, Hkv, D, cos_t, sin_t, kc1, vt1, cnt1, scale, workspace=ws,
+                                 mask=mask, n_keys=T)
+    kc2, vt2 = dev_bf16(k), dev_bf16(vt_h)
+    cnt2 = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    qkv2 = dev_bf16(rows)
+    _lib.rope_append_kv(qkv2, B, 1, H, Hkv, D, cos_t, sin_t, kc2, vt2, cnt2)
+    out2 = _lib.attention(qkv2, B, 1, H, Hkv, D, kc2, vt2, cnt2, scale, workspace=ws, mask=mask, n_keys=T)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vt1, vt2)
+    a, b2 = bf16_to_f32(host_u16(out1)), bf16_to_f32(host_u16(out2))
+    assert np.isfinite(a).all()
+    assert np.abs(a - b2).max() <= 1e-2 * np.abs(b2).max()
+    kh = bf16_to_f32(host_u16(kc1)[:, :, :T])
+    vh = bf16_to_f32(host_u16(vt1)[:, :, :, :T]).transpose(0, 1, 3, 2)
+    cos, sin = rope_cos_sin(np.array([past]), D, 500000.0)
+    q = bf16_to_f32(rows[:, :H * D]).reshape(B, 1, H, D).transpose(0, 2, 1, 3)
+    q = bf16_to_f32(f32_to_bf16(apply_rope(q, cos, sin)))
+    rep = H // Hkv
+    ref = attention_core(q, np.repeat(kh, rep, axis=1), np.repeat(vh, rep, axis=1), scale, T - 1, mask=m)
+    ref = ref.transpose(0, 2, 1, 3).reshape(B, H * D)
+    assert np.abs(a - ref).max() / np.abs(ref).max() <= ATTN_TOL
+
+
+def test_attention_decode_mask_all_inf_row_is_nan(device):
+    # every visible key -inf: 0 / 0, as the reference's softmax gives
+    B, H, Hkv, D, past = 1, 8, 2, 128, 20
+    rng = np.random.default_rng(9)
+    rows, k, v, cos_t, sin_t = _decode_case(rng, B, H, Hkv, D, past, 64)
+    mask = torch.full((1, 1, 1, past + 1), -float("inf"), device="cuda")
+    cnt = torch.tensor([past, 0], dtype=torch.int32, device="cuda")
+    out = _lib.attention_decode(dev_bf16(rows), B, H, Hkv, D, cos_t, sin_t, dev_bf16(k),
+                                dev_bf16(np.ascontiguousarray(v.transpose(0, 1, 3, 2))), cnt, 0.1, mask=mask,
+                                n_keys=past + 1)
+    torch.cuda.synchronize()
+    assert torch.isnan(out.float()).all()
