@@ -34,8 +34,8 @@ extern "C" {
 #define SC_ABI_VERSION 13
 
 /* Kernel selection for sc_qmm_bf16_path. */
-#define SC_QMM_PATH_AUTO 0 /* M <= 32: GEMV or band kernel (8-32 rows, by shape);
-                              33-160: band kernel; above: GEMM                  */
+#define SC_QMM_PATH_AUTO 0 /* M <= 16: GEMV or band kernel (8-16 rows, by shape);
+                              17-160: band kernel; above: GEMM                  */
 #define SC_QMM_PATH_GEMV 1 /* fused dequant-GEMV (decode batches, M <= 32)      */
 #define SC_QMM_PATH_GEMM 2 /* LDS-staged dequant -> bf16 MFMA GEMM (prefill)     */
 #define SC_QMM_PATH_BAND 3 /* weight-streaming band kernel (M <= 256)            */

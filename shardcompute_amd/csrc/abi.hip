@@ -162,17 +162,19 @@ static int check_qmm(const void *x, const void *wq, const void *s, const void *b
 }
 
 // Whether the automatic choice is the band kernel: 33-160 rows (measured faster than
-// the GEMM's 256-row tiles up to 128 rows, slower at 256); 9-32 rows where the
-// 16-column GEMV's K splits or x staging cost more than the band's stream: K above
-// 4096 or at most 8192 weight rows (measured on the decode shapes: 8B down at 16
-// rows 17 against 25 us, the 70B shard's q|k|v, gate|up and down at 32 rows 10, 19, 13
-// against 11, 23, 15 us; 8B gate|up at 16 rows 29 against 24 us stays on the GEMV);
+// the GEMM's 256-row tiles up to 128 rows, slower at 256); 17-32 rows, where both
+// kernels compute 32 rows and the band's stream is the faster (8B gate|up at 20, 24
+// and 32 rows 28, 31, 30 against 32, 34, 34 us on the GEMV; the 8B lm_head at 32 rows
+// 99 against 119 us); 9-16 rows where the 16-column GEMV's K splits or x staging cost
+// more than the band's stream: K above 4096 or at most 8192 weight rows (8B down at 16
+// rows 17 against 25 us; 8B gate|up at 16 rows 29 against 24 us and the lm_head 95
+// against 73 us stay on the GEMV, which computes 16 rows where the band computes 32);
 // and 8 rows with K of 4096 or more (8B q|k|v, gate|up, down 10, 15, 16 against 12,
 // 17, 26 us on the 8-row GEMV; K = 2048 is a tie).
 static bool band_first(int64_t M, int64_t N, int64_t K) {
     if (M > 32) return M <= 160;
     if (M == 8) return K >= 4096;
-    return M > 8 && (K > 4096 || N <= 8192);
+    return M > 16 || (M > 8 && (K > 4096 || N <= 8192));
 }
 
 static int qmm_dispatch(const uint16_t *x, const uint32_t *wq, const uint16_t *s, const uint16_t *b,
