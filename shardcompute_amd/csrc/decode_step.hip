@@ -1010,6 +1010,11 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     if (ac == newk) kv[u] = kn;
                 }
             }
+            // V^T rows (dim 16 n + ac, keys 0..7): read now, so the reads overlap S and the softmax
+            const uint4 *vrow = reinterpret_cast<const uint4 *>(sl + 2048 + ac * 16);
+            uint4 vv[D / 16];
+#pragma unroll
+            for (int n = 0; n < D / 16; ++n) vv[n] = vrow[16 * n];
             f4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int u = 0; u < D / 32; ++u)
@@ -1043,38 +1048,44 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             // for the others (their B is zero, and a zero A keeps them finite).  Block
             // with the new key: its value comes from LDS; keys past the range are zeroed
             // (their p is 0; cache slots past the length may hold anything).
-            const uint4 *vrow = reinterpret_cast<const uint4 *>(sl + 2048 + ac * 16);
-            const bool live = ag == 0;
+            // lanes of k groups 1..3 are zeroed with a register mask, not a branch: a
+            // branch over an operand with its LDS read in flight waits for that read, and
+            // the eight reads of the block then run one after another
+            uint32_t lm = ag == 0 ? 0xFFFFFFFFu : 0u;
+            asm volatile("" : "+v"(lm));
             if (!has_new && nval == 8) {
+                f4 o[D / 16];
 #pragma unroll
                 for (int n = 0; n < D / 16; ++n) {
-                    uint4 vv = vrow[16 * n];
-                    if (!live) vv = make_uint4(0u, 0u, 0u, 0u);
-                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), pb8, f4{0.f, 0.f, 0.f, 0.f},
-                                                                         0, 0, 0);
-                    // lane (head ac, ag): dims 16 n + 4 ag + r
-                    if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
+                    vv[n] = make_uint4(vv[n].x & lm, vv[n].y & lm, vv[n].z & lm, vv[n].w & lm);
+                    o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv[n]), pb8, f4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                                   0, 0);
                 }
+                // lane (head ac, ag): dims 16 n + 4 ag + r
+                if (ac < R)
+#pragma unroll
+                    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o[n];
             } else {
                 uint32_t km[4];                                // per word: its elements < nval
 #pragma unroll
                 for (int w = 0; w < 4; ++w)
-                    km[w] = nval >= 2 * w + 2 ? 0xFFFFFFFFu : nval == 2 * w + 1 ? 0x0000FFFFu : 0u;
+                    km[w] = (nval >= 2 * w + 2 ? 0xFFFFFFFFu : nval == 2 * w + 1 ? 0x0000FFFFu : 0u) & lm;
                 uint32_t nm[4];                                // per word: the new key's half
 #pragma unroll
                 for (int w = 0; w < 4; ++w) nm[w] = (has_new && (newk >> 1) == w) ? (0xFFFFu << ((newk & 1) * 16)) : 0u;
                 const int nsh = (newk & 1) * 16;
                 const uint16_t *vnew = qkv_l + RMAX * D + D + ac;
+                uint32_t nv[D / 16];
+#pragma unroll
+                for (int n = 0; n < D / 16; ++n) nv[n] = (uint32_t)vnew[16 * n] << nsh;
 #pragma unroll
                 for (int n = 0; n < D / 16; ++n) {
-                    uint4 vv = vrow[16 * n];
-                    const uint32_t nv = (uint32_t)vnew[16 * n] << nsh;
-                    vv.x = ((vv.x & ~nm[0]) | (nv & nm[0])) & km[0];
-                    vv.y = ((vv.y & ~nm[1]) | (nv & nm[1])) & km[1];
-                    vv.z = ((vv.z & ~nm[2]) | (nv & nm[2])) & km[2];
-                    vv.w = ((vv.w & ~nm[3]) | (nv & nm[3])) & km[3];
-                    if (!live) vv = make_uint4(0u, 0u, 0u, 0u);
-                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv), pb8, f4{0.f, 0.f, 0.f, 0.f},
+                    uint4 v = vv[n];
+                    v.x = ((v.x & ~nm[0]) | (nv[n] & nm[0])) & km[0];
+                    v.y = ((v.y & ~nm[1]) | (nv[n] & nm[1])) & km[1];
+                    v.z = ((v.z & ~nm[2]) | (nv[n] & nm[2])) & km[2];
+                    v.w = ((v.w & ~nm[3]) | (nv[n] & nm[3])) & km[3];
+                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v), pb8, f4{0.f, 0.f, 0.f, 0.f},
                                                                          0, 0, 0);
                     if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
                 }
