@@ -107,7 +107,6 @@ struct Args {
     int L, nops, hidden, H, Hkv, R, NR, T_cap, C_merge;
     float eps, scale_log2;
     // LDS layout (byte offsets into dynamic shared memory)
-    int n_items;            // attention items per unit at most (keys per unit / 8)
     int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
     uint32_t *trace;          // null, or [P][nops][4] real-time stamps of the last launch
 };
@@ -398,17 +397,21 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
 
     // Every wave: gather the raw chunks of a wide input (chunk c = LL words [4c, 4c + 4) of
     // src) into x, the blocks of 64 chunks dealt round-robin to the nine waves (at most 4
-    // per wave).  Chunks that are not all there are then watched through their last word
-    // only, with a short sleep between polls, and re-read once it carries the epoch: 2304
-    // waves re-reading whole inputs would flood L2 ahead of the producers' weight reads.
-    // A worker's waits here also cover its older weight DMA (vmcnt retires in order).
+    // per wave).  A chunk is watched through its last word only, with a short sleep
+    // between polls, and read whole once that word carries the epoch: 2304 waves reading
+    // whole inputs flood the memory path ahead of the producers' publishes and weight
+    // reads.  Even a first whole read is not worth its bytes: the waves get here right
+    // after their own workgroup's last item, before most producers have published
+    // (8B step 1.674 -> 1.634 ms, TinyLlama 0.764 -> 0.741 ms against reading every chunk
+    // whole first).  A worker's waits here also cover its older weight DMA (vmcnt retires
+    // in order).
     auto gather_all = [&](const uint2 *src, int n8, uint32_t ep) __attribute__((always_inline)) -> bool {
         constexpr int NW = WORKERS + 1;
         uint32_t pend = 0u;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
             if ((wave + NW * i) * 64 + lane < n8) pend |= 1u << i;
-        uint32_t fetch = pend;                          // chunks to read whole this round
+        uint32_t fetch = 0u;                            // chunks to read whole this round
         const uint2 *wsrc = src + 4 * 64 * wave;        // wave-uniform base + lane offset
         const uint32_t lane_w = 4u * lane;
         for (int it = 0;; ++it) {
@@ -496,48 +499,45 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 if (au.valid) {
                     // merge the items' (m, l, O) per head, in item order (the same sums
                     // whichever wave computed which item), into part: [R][D + 2] = O
-                    // (unnormalised), m, l.  First each item's weight exp2(m_i - M) per
-                    // head (fac[h][i], M at mh[h]), then one fma per item and value.
+                    // (unnormalised), m, l.  Each value's thread takes the head's maximum M
+                    // over the items and weighs item i by exp2(m_i - M), one fma per item:
+                    // one pass (the maxima are broadcast reads), no barrier inside.
                     const int ni = au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
                     uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
-                    float *fac = part + RMAX * (D + 2), *mh = fac + RMAX * a.n_items;
-                    for (int t = tid; t < a.R * ni; t += THREADS) {
-                        const int h = t / ni, w = t - h * ni;
+                    for (int t = tid; t < a.R * (D + 2); t += THREADS) {
+                        const int h = t / (D + 2), x = t - h * (D + 2);
+                        const float *mrow = ast + h * (D + 4) + D;
                         float M = -INFINITY;
                         int v = 0;
                         for (; v + 4 <= ni; v += 4) {              // reads 4 at a time
-                            float t[4];
+                            float m4[4];
 #pragma unroll
-                            for (int k = 0; k < 4; ++k) t[k] = ast[(v + k) * AST + h * (D + 4) + D];
+                            for (int k = 0; k < 4; ++k) m4[k] = mrow[(v + k) * AST];
 #pragma unroll
-                            for (int k = 0; k < 4; ++k) M = fmaxf(M, t[k]);
+                            for (int k = 0; k < 4; ++k) M = fmaxf(M, m4[k]);
                         }
-                        for (; v < ni; ++v) M = fmaxf(M, ast[v * AST + h * (D + 4) + D]);
-                        const float mw = ast[w * AST + h * (D + 4) + D];
-                        fac[h * ni + w] = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-                        if (w == 0) mh[h] = M;
-                    }
-                    __syncthreads();
-                    for (int t = tid; t < a.R * (D + 2); t += THREADS) {
-                        const int h = t / (D + 2), x = t - h * (D + 2);
+                        for (; v < ni; ++v) M = fmaxf(M, mrow[v * AST]);
                         float acc = 0.f;
                         if (x == D) {
-                            acc = ni > 0 ? mh[h] : -INFINITY;
+                            acc = ni > 0 ? M : -INFINITY;
                         } else {
                             const float *src = ast + h * (D + 4) + x;          // x = D + 1: l
-                            const float *fh = fac + h * ni;
                             int w = 0;
                             for (; w + 4 <= ni; w += 4) {          // reads 4 items at a time
-                                float f[4], o[4];
+                                float mw[4], o[4];
 #pragma unroll
                                 for (int k = 0; k < 4; ++k) {
-                                    f[k] = fh[w + k];
+                                    mw[k] = mrow[(w + k) * AST];
                                     o[k] = src[(w + k) * AST];
                                 }
 #pragma unroll
-                                for (int k = 0; k < 4; ++k) acc = fmaf(f[k], o[k], acc);
+                                for (int k = 0; k < 4; ++k)
+                                    acc = fmaf((mw[k] == -INFINITY) ? 0.f : exp2f(mw[k] - M), o[k], acc);
                             }
-                            for (; w < ni; ++w) acc = fmaf(fh[w], src[w * AST], acc);
+                            for (; w < ni; ++w) {
+                                const float mw = mrow[w * AST];
+                                acc = fmaf((mw == -INFINITY) ? 0.f : exp2f(mw - M), src[w * AST], acc);
+                            }
                         }
                         part[t] = acc;
                     }
@@ -1261,16 +1261,14 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     size_t off = (size_t)WORKERS * TRING * SLOT;
     // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 2) floats
     const int kps_max = ((m->T_cap + NR - 1) / NR + 7) & ~7;
-    const int n_items = kps_max / 8;
-    a.n_items = n_items;
+    const int n_items = kps_max / 8;            // attention items per unit at most
     const size_t ast_bytes = (size_t)n_items * RMAX * (D + 4) * 4;
     a.o_xl = (int)off; off += align16(std::max((size_t)Kmax * 2, ast_bytes));
     a.o_xzero = (int)off; off += 1024;
     a.o_xs = (int)off; off += align16((size_t)(Kmax / 64) * 4);
     // projection partials, or the attention merge [RMAX][D + 2]
-    // (attention: the merge [RMAX][D + 2], its weights [RMAX][n_items] and maxima [RMAX])
     a.o_part = (int)off;
-    off += align16(std::max((size_t)max_items * 64, ((size_t)RMAX * (D + 2) + (size_t)RMAX * n_items + RMAX) * 4));
+    off += align16(std::max((size_t)max_items * 64, (size_t)RMAX * (D + 2) * 4));
     a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
     a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
     a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
