@@ -36,6 +36,7 @@
 // remaining work (its waves still pass every op boundary together), drains its DMA
 // and ends.
 #include <algorithm>
+#include <cstdlib>
 #include <memory>
 #include <vector>
 
@@ -108,6 +109,7 @@ struct Args {
     float eps, scale_log2;
     // LDS layout (byte offsets into dynamic shared memory)
     int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
+    int o_spare;            // the control wave's attention item area (in x's), or -1
     uint32_t *trace;          // null, or [P][nops][4] real-time stamps of the last launch
 };
 
@@ -264,6 +266,15 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     kps = (kps + 7) & ~7;
     const uint32_t base = a.epoch_base[0];
     const AttnUnit au = attn_unit(a, wg, T, kps);
+    // The unit's attention items.  With more than there are workers (9 for 8 workers
+    // at 2049-2304 positions on the Llama-3-8B shape), the control wave, idle while
+    // the items are computed, takes the last one: loaded into its own LDS area while
+    // q|k|v is computed, so the op needs one round of items instead of two.
+    const int ni_unit = au.valid && au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
+    // (head_dim 128 only: at 64 the x area rarely has room beside the states, and the
+    // code in the control wave's path costs the other instantiation's boundaries
+    // registers: TinyLlama 0.741 -> 0.746 ms a step with it compiled in)
+    const bool ctl_item = D == 128 && a.o_spare >= 0 && ni_unit > WORKERS;
 
     // ---- set-up by the control wave: shapes and layer pointers into LDS, this
     // workgroup's items per op kind; then the one workgroup-wide barrier
@@ -288,7 +299,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 s_pre[k] = acc;
                 int n = 0;
                 if (k == K_ATTN) {
-                    if (au.valid && au.lo < au.hi) n = (au.hi - au.lo + 7) >> 3;
+                    n = ni_unit - (ctl_item ? 1 : 0);
                 } else if (k != K_MERGE) {
                     const int gi = gemv_index(k);
                     const GemvDesc g = gi == 0 ? a.gd[0] : gi == 1 ? a.gd[1] : gi == 2 ? a.gd[2] : a.gd[3];
@@ -812,6 +823,31 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     struct ItemLoc {
         int l, k, i, ch;
     };
+    // DMA of attention item i of this workgroup's unit (layer lp) to LDS dst
+    auto dma_attn = [&](const LayerPtrs &lp, int i, uint32_t dst) __attribute__((always_inline)) {
+        const uint32_t d1 = dst + 1024, d2 = dst + 2048, d3 = dst + 3072, d4 = dst + 4096;
+        // 8 cached keys: K rows [kb, kb + 8) (D 2 bytes each, from the slot's start; row r's
+        // 16-byte chunks rotated by r, so the 8 rows' same chunk sits in different banks)
+        // and V^T columns (D x 16 B, from byte 2048).  head_dim 64 fills half of each;
+        // the other instructions reload the same bytes, so every item issues five.
+        const int kb = au.lo + 8 * i;
+        const uint8_t *kp = reinterpret_cast<const uint8_t *>(lp.kc + ((size_t)au.kvh * a.T_cap + kb) * D);
+        const uint16_t *vp = lp.vt + (size_t)au.kvh * D * a.T_cap + kb;
+        if (D == 128) {
+            const int kr0 = lane >> 4, kr1 = 4 + (lane >> 4);
+            dma16(kp + kr0 * 256 + (((lane & 15) + kr0) & 15) * 16, dst);
+            dma16(kp + kr1 * 256 + (((lane & 15) + kr1) & 15) * 16, d1);
+            dma16(vp + (size_t)lane * a.T_cap, d2);
+            dma16(vp + (size_t)(64 + lane) * a.T_cap, d3);
+        } else {
+            const int kr = lane >> 3;
+            dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
+            dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
+            dma16(vp + (size_t)lane * a.T_cap, d2);
+            dma16(vp + (size_t)lane * a.T_cap, d2);
+        }
+        if (lane < 32) dma16(kp + 16 * lane, d4);
+    };
     // DMA of item g to LDS dst: 4 weight instructions + 1 scale/bias (or 4 key/value + 1
     // filler) instructions.
     auto dma_item = [&](int g, uint32_t dst) __attribute__((always_inline)) -> ItemLoc {
@@ -858,33 +894,157 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             if (lane < 32)
                 dma16((lane < 16 ? lp.s[gi] : lp.b[gi]) + (wrow(lane & 15) * G + (uint32_t)((ch * ITEM_GROUPS) & ~7)), d4);
         } else {
-            // 8 cached keys: K rows [kb, kb + 8) (D 2 bytes each, from the slot's start; row r's
-            // 16-byte chunks rotated by r, so the 8 rows' same chunk sits in different banks)
-            // and V^T columns (D x 16 B, from byte 2048).  head_dim 64 fills half of each;
-            // the other instructions reload the same bytes, so every item issues five.
-            const int kb = au.lo + 8 * w.i;
-            const uint8_t *kp = reinterpret_cast<const uint8_t *>(lp.kc + ((size_t)au.kvh * a.T_cap + kb) * D);
-            const uint16_t *vp = lp.vt + (size_t)au.kvh * D * a.T_cap + kb;
-            if (D == 128) {
-                const int kr0 = lane >> 4, kr1 = 4 + (lane >> 4);
-                dma16(kp + kr0 * 256 + (((lane & 15) + kr0) & 15) * 16, dst);
-                dma16(kp + kr1 * 256 + (((lane & 15) + kr1) & 15) * 16, d1);
-                dma16(vp + (size_t)lane * a.T_cap, d2);
-                dma16(vp + (size_t)(64 + lane) * a.T_cap, d3);
-            } else {
-                const int kr = lane >> 3;
-                dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
-                dma16(kp + kr * 128 + (((lane & 7) + kr) & 7) * 16, dst);
-                dma16(vp + (size_t)lane * a.T_cap, d2);
-                dma16(vp + (size_t)lane * a.T_cap, d2);
-            }
-            if (lane < 32) dma16(kp + 16 * lane, d4);
+            dma_attn(lp, w.i, dst);
         }
         return w;
     };
 
+    // ---- attention item: 8 keys of kv head au.kvh against its R query heads, on MFMA
+    //   S^T[16 key rows (8 used) x 16 head columns (R used)] = K . Q^T   (4 x 16x16x32)
+    //   p = exp2(S^T scale - max), per head over the 8 keys (fp32; l sums fp32 p)
+    //   O^T[D x 16 heads] = V^T[D x keys] . P^T with P in bf16     (8 x 16x16x32)
+    // as the per-op attention kernel computes a block.  The item's (m, l, O) per head
+    // goes to state block i ([RMAX][D + 4] floats); the op's epilogue merges the
+    // blocks in item order, so the sums do not depend on which wave took which item.
+    // sl: the item's bytes in LDS (a worker's ring slot, or the control wave's item
+    // area).  ac: MFMA column (key row of A, head column of B), ag: its k group.
+    auto attn_compute = [&](int i, const uint8_t *sl) {
+        const int R = a.R;
+        // recomputed per item: hoisted out of the item loop, the per-tile addresses
+        // would be held (and spilled) across the whole stream
+        int ac = lane & 15;
+        asm volatile("" : "+v"(ac));
+        const int ag = lane >> 4;
+        float *stw = ast + i * AST;
+        const int kb = au.lo + 8 * i;
+        const int nval = min(8, au.hi - kb);               // valid keys of the block, wave-uniform
+        const int newk = T - 1 - kb;                       // the new key's slot in the block, if 0..7
+        const bool has_new = newk >= 0 && newk < 8;        // wave-uniform
+        // operand A: key row ac, chunk 4u + ag (cached row r's chunk c sits at slot
+        // (c - r) & 15; rows 8..15 read the block's V^T bytes: their S rows are
+        // masked, and MFMA rows do not mix).  The new key is not in the cache yet:
+        // its rotated copy is in LDS.  Operand B: query head min(ac, R - 1), the same
+        // chunk (columns past R are ignored).
+        const uint4 *krow = reinterpret_cast<const uint4 *>(sl + ac * (2 * D));
+        const uint4 *qrow = reinterpret_cast<const uint4 *>(qkv_l + min(ac, R - 1) * D);
+        uint4 kv[D / 32], qv[D / 32];
+#pragma unroll
+        for (int u = 0; u < D / 32; ++u) {
+            kv[u] = krow[(4 * u + ag - ac) & (KCH - 1)];
+            qv[u] = qrow[4 * u + ag];
+        }
+        if (has_new) {
+            const uint4 *knew = reinterpret_cast<const uint4 *>(qkv_l + RMAX * D);
+#pragma unroll
+            for (int u = 0; u < D / 32; ++u) {
+                const uint4 kn = knew[4 * u + ag];
+                if (ac == newk) kv[u] = kn;
+            }
+        }
+        // V^T rows (dim 16 n + ac, keys 0..7): read now, so the reads overlap S and the softmax
+        const uint4 *vrow = reinterpret_cast<const uint4 *>(sl + 2048 + ac * 16);
+        uint4 vv[D / 16];
+#pragma unroll
+        for (int n = 0; n < D / 16; ++n) vv[n] = vrow[16 * n];
+        f4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < D / 32; ++u)
+            st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[u]), as_bf16x8(qv[u]), st, 0, 0, 0);
+        // lane (ac = head, ag): keys 4 ag + r; keys 0-3 in lanes 0-15, 4-7 in lanes 16-31
+        float sv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sv[r] = (4 * ag + r < nval) ? st[r] * a.scale_log2 : -INFINITY;
+        float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+        float x0, x1;
+        swap16(bm, x0, x1);
+        bm = fmaxf(x0, x1);                                // rows 0, 1: the max over the 8 keys
+        float pv[4], ps = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pv[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - bm);
+            ps += pv[r];
+        }
+        swap16(ps, x0, x1);
+        ps = x0 + x1;
+        // operand B of O^T: lane (head ac, k group 0) holds keys 0..7 as bf16, the
+        // other k groups zero
+        float pk[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) swap16(pv[r], pk[r], pk[4 + r]);
+        uint4 pw = make_uint4(cvt_pk_bf16(pk[0], pk[1]), cvt_pk_bf16(pk[2], pk[3]), cvt_pk_bf16(pk[4], pk[5]),
+                              cvt_pk_bf16(pk[6], pk[7]));
+        if (ag != 0) pw = make_uint4(0u, 0u, 0u, 0u);
+        const bf16x8_t pb8 = as_bf16x8(pw);
+        // operand A of O^T: V^T row (dim 16 n + ac) over keys 0..7 for k group 0, zero
+        // for the others (their B is zero, and a zero A keeps them finite).  Block
+        // with the new key: its value comes from LDS; keys past the range are zeroed
+        // (their p is 0; cache slots past the length may hold anything).
+        // lanes of k groups 1..3 are zeroed with a register mask, not a branch: a
+        // branch over an operand with its LDS read in flight waits for that read, and
+        // the eight reads of the block then run one after another
+        uint32_t lm = ag == 0 ? 0xFFFFFFFFu : 0u;
+        asm volatile("" : "+v"(lm));
+        if (!has_new && nval == 8) {
+            f4 o[D / 16];
+#pragma unroll
+            for (int n = 0; n < D / 16; ++n) {
+                vv[n] = make_uint4(vv[n].x & lm, vv[n].y & lm, vv[n].z & lm, vv[n].w & lm);
+                o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv[n]), pb8, f4{0.f, 0.f, 0.f, 0.f}, 0,
+                                                               0, 0);
+            }
+            // lane (head ac, ag): dims 16 n + 4 ag + r
+            if (ac < R)
+#pragma unroll
+                for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o[n];
+        } else {
+            uint32_t km[4];                                // per word: its elements < nval
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                km[w] = (nval >= 2 * w + 2 ? 0xFFFFFFFFu : nval == 2 * w + 1 ? 0x0000FFFFu : 0u) & lm;
+            uint32_t nm[4];                                // per word: the new key's half
+#pragma unroll
+            for (int w = 0; w < 4; ++w) nm[w] = (has_new && (newk >> 1) == w) ? (0xFFFFu << ((newk & 1) * 16)) : 0u;
+            const int nsh = (newk & 1) * 16;
+            const uint16_t *vnew = qkv_l + RMAX * D + D + ac;
+            uint32_t nv[D / 16];
+#pragma unroll
+            for (int n = 0; n < D / 16; ++n) nv[n] = (uint32_t)vnew[16 * n] << nsh;
+#pragma unroll
+            for (int n = 0; n < D / 16; ++n) {
+                uint4 v = vv[n];
+                v.x = ((v.x & ~nm[0]) | (nv[n] & nm[0])) & km[0];
+                v.y = ((v.y & ~nm[1]) | (nv[n] & nm[1])) & km[1];
+                v.z = ((v.z & ~nm[2]) | (nv[n] & nm[2])) & km[2];
+                v.w = ((v.w & ~nm[3]) | (nv[n] & nm[3])) & km[3];
+                const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v), pb8, f4{0.f, 0.f, 0.f, 0.f},
+                                                                     0, 0, 0);
+                if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
+            }
+        }
+        if (ac < R && ag == 0) {
+            stw[ac * (D + 4) + D] = bm;
+            stw[ac * (D + 4) + D + 1] = ps;
+        }
+    };
+
     if (wave == CTL) {
-        for (int jj = 0; jj <= nops; ++jj) boundary(jj, std::true_type{});
+        const uint8_t *own = smem + (ctl_item ? a.o_spare : 0);
+        for (int jj = 0; jj <= nops; ++jj) {
+            boundary(jj, std::true_type{});
+            if (D == 128 && ctl_item && jj >= 1 && jj < nops && !s_abort) {
+                // the x area past q|k|v's input and the attention states is free from
+                // q|k|v's staging (the previous layer's down input is dead) until this
+                // layer's attention items are merged
+                const int k = kind_of(jj);
+                if (k == K_QKV) {
+                    dma_attn(slp[(jj - 1) / NT], ni_unit - 1, (uint32_t)(uintptr_t)own);
+                } else if (k == K_ATTN) {
+                    wait_vm<0>();
+                    attn_compute(ni_unit - 1, own);
+                }
+            }
+        }
+        wait_vm<0>();                                   // no DMA may land after the workgroup ends
         if (lane == 0 && s_abort) atomicOr(a.status, 2u);
         if (wg == 0 && lane == 0) {
             // every workgroup read the base before producing anything, and workgroup 0
@@ -968,133 +1128,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             if (q == 0) part[i * 16 + j16] = acc;
         };
 
-        // ---- attention item: 8 keys of kv head au.kvh against its R query heads, on MFMA
-        //   S^T[16 key rows (8 used) x 16 head columns (R used)] = K . Q^T   (4 x 16x16x32)
-        //   p = exp2(S^T scale - max), per head over the 8 keys (fp32; l sums fp32 p)
-        //   O^T[D x 16 heads] = V^T[D x keys] . P^T with P in bf16     (8 x 16x16x32)
-        // as the per-op attention kernel computes a block.  The item's (m, l, O) per head
-        // goes to state block i ([RMAX][D + 4] floats); the op's epilogue merges the
-        // blocks in item order, so the sums do not depend on which wave took which item.
-        // ac: MFMA column (key row of A, head column of B), ag: its k group.
-        const int R = a.R;
-        auto attn_item = [&](int i, int slot) {
-            // recomputed per item: hoisted out of the item loop, the per-tile addresses
-            // would be held (and spilled) across the whole stream
-            int ac = lane & 15;
-            asm volatile("" : "+v"(ac));
-            const int ag = lane >> 4;
-            float *stw = ast + i * AST;
-            const uint8_t *sl = ring + slot * SLOT;
-            const int kb = au.lo + 8 * i;
-            const int nval = min(8, au.hi - kb);               // valid keys of the block, wave-uniform
-            const int newk = T - 1 - kb;                       // the new key's slot in the block, if 0..7
-            const bool has_new = newk >= 0 && newk < 8;        // wave-uniform
-            // operand A: key row ac, chunk 4u + ag (cached row r's chunk c sits at slot
-            // (c - r) & 15; rows 8..15 read the block's V^T bytes: their S rows are
-            // masked, and MFMA rows do not mix).  The new key is not in the cache yet:
-            // its rotated copy is in LDS.  Operand B: query head min(ac, R - 1), the same
-            // chunk (columns past R are ignored).
-            const uint4 *krow = reinterpret_cast<const uint4 *>(sl + ac * (2 * D));
-            const uint4 *qrow = reinterpret_cast<const uint4 *>(qkv_l + min(ac, R - 1) * D);
-            uint4 kv[D / 32], qv[D / 32];
-#pragma unroll
-            for (int u = 0; u < D / 32; ++u) {
-                kv[u] = krow[(4 * u + ag - ac) & (KCH - 1)];
-                qv[u] = qrow[4 * u + ag];
-            }
-            if (has_new) {
-                const uint4 *knew = reinterpret_cast<const uint4 *>(qkv_l + RMAX * D);
-#pragma unroll
-                for (int u = 0; u < D / 32; ++u) {
-                    const uint4 kn = knew[4 * u + ag];
-                    if (ac == newk) kv[u] = kn;
-                }
-            }
-            // V^T rows (dim 16 n + ac, keys 0..7): read now, so the reads overlap S and the softmax
-            const uint4 *vrow = reinterpret_cast<const uint4 *>(sl + 2048 + ac * 16);
-            uint4 vv[D / 16];
-#pragma unroll
-            for (int n = 0; n < D / 16; ++n) vv[n] = vrow[16 * n];
-            f4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int u = 0; u < D / 32; ++u)
-                st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kv[u]), as_bf16x8(qv[u]), st, 0, 0, 0);
-            // lane (ac = head, ag): keys 4 ag + r; keys 0-3 in lanes 0-15, 4-7 in lanes 16-31
-            float sv[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sv[r] = (4 * ag + r < nval) ? st[r] * a.scale_log2 : -INFINITY;
-            float bm = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-            float x0, x1;
-            swap16(bm, x0, x1);
-            bm = fmaxf(x0, x1);                                // rows 0, 1: the max over the 8 keys
-            float pv[4], ps = 0.f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pv[r] = (sv[r] == -INFINITY) ? 0.f : exp2f(sv[r] - bm);
-                ps += pv[r];
-            }
-            swap16(ps, x0, x1);
-            ps = x0 + x1;
-            // operand B of O^T: lane (head ac, k group 0) holds keys 0..7 as bf16, the
-            // other k groups zero
-            float pk[8];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) swap16(pv[r], pk[r], pk[4 + r]);
-            uint4 pw = make_uint4(cvt_pk_bf16(pk[0], pk[1]), cvt_pk_bf16(pk[2], pk[3]), cvt_pk_bf16(pk[4], pk[5]),
-                                  cvt_pk_bf16(pk[6], pk[7]));
-            if (ag != 0) pw = make_uint4(0u, 0u, 0u, 0u);
-            const bf16x8_t pb8 = as_bf16x8(pw);
-            // operand A of O^T: V^T row (dim 16 n + ac) over keys 0..7 for k group 0, zero
-            // for the others (their B is zero, and a zero A keeps them finite).  Block
-            // with the new key: its value comes from LDS; keys past the range are zeroed
-            // (their p is 0; cache slots past the length may hold anything).
-            // lanes of k groups 1..3 are zeroed with a register mask, not a branch: a
-            // branch over an operand with its LDS read in flight waits for that read, and
-            // the eight reads of the block then run one after another
-            uint32_t lm = ag == 0 ? 0xFFFFFFFFu : 0u;
-            asm volatile("" : "+v"(lm));
-            if (!has_new && nval == 8) {
-                f4 o[D / 16];
-#pragma unroll
-                for (int n = 0; n < D / 16; ++n) {
-                    vv[n] = make_uint4(vv[n].x & lm, vv[n].y & lm, vv[n].z & lm, vv[n].w & lm);
-                    o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(vv[n]), pb8, f4{0.f, 0.f, 0.f, 0.f}, 0,
-                                                                   0, 0);
-                }
-                // lane (head ac, ag): dims 16 n + 4 ag + r
-                if (ac < R)
-#pragma unroll
-                    for (int n = 0; n < D / 16; ++n) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o[n];
-            } else {
-                uint32_t km[4];                                // per word: its elements < nval
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    km[w] = (nval >= 2 * w + 2 ? 0xFFFFFFFFu : nval == 2 * w + 1 ? 0x0000FFFFu : 0u) & lm;
-                uint32_t nm[4];                                // per word: the new key's half
-#pragma unroll
-                for (int w = 0; w < 4; ++w) nm[w] = (has_new && (newk >> 1) == w) ? (0xFFFFu << ((newk & 1) * 16)) : 0u;
-                const int nsh = (newk & 1) * 16;
-                const uint16_t *vnew = qkv_l + RMAX * D + D + ac;
-                uint32_t nv[D / 16];
-#pragma unroll
-                for (int n = 0; n < D / 16; ++n) nv[n] = (uint32_t)vnew[16 * n] << nsh;
-#pragma unroll
-                for (int n = 0; n < D / 16; ++n) {
-                    uint4 v = vv[n];
-                    v.x = ((v.x & ~nm[0]) | (nv[n] & nm[0])) & km[0];
-                    v.y = ((v.y & ~nm[1]) | (nv[n] & nm[1])) & km[1];
-                    v.z = ((v.z & ~nm[2]) | (nv[n] & nm[2])) & km[2];
-                    v.w = ((v.w & ~nm[3]) | (nv[n] & nm[3])) & km[3];
-                    const f4 o = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(v), pb8, f4{0.f, 0.f, 0.f, 0.f},
-                                                                         0, 0, 0);
-                    if (ac < R) *reinterpret_cast<f4 *>(stw + ac * (D + 4) + 16 * n + 4 * ag) = o;
-                }
-            }
-            if (ac < R && ag == 0) {
-                stw[ac * (D + 4) + D] = bm;
-                stw[ac * (D + 4) + D + 1] = ps;
-            }
-        };
+        auto attn_item = [&](int i, int slot) { attn_compute(i, ring + slot * SLOT); };
 
         // Every op boundary up to and including op k's staging, before the item of op
         // k is awaited: the other waves need not wait for this wave's next DMA.
@@ -1266,6 +1300,17 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     a.o_xl = (int)off; off += align16(std::max((size_t)Kmax * 2, ast_bytes));
     a.o_xzero = (int)off; off += 1024;
     a.o_xs = (int)off; off += align16((size_t)(Kmax / 64) * 4);
+    // the control wave's attention item (one ring slot), in the x area past q|k|v's
+    // input and the attention states, when it fits there.  SC_TRUNK_CONTROL_ITEM=0 in
+    // the environment at plan creation leaves every item to the workers (the results
+    // are the same bits: the states merge in item order whoever computed them).
+    {
+        const size_t xarea = align16(std::max((size_t)Kmax * 2, ast_bytes));
+        const size_t rel = align16(std::max(ast_bytes, (size_t)hid * 2));
+        a.o_spare = rel + SLOT <= xarea ? (int)(a.o_xl + rel) : -1;
+        const char *ev = getenv("SC_TRUNK_CONTROL_ITEM");
+        if (ev && ev[0] == '0') a.o_spare = -1;
+    }
     // projection partials, or the attention merge [RMAX][D + 2]
     a.o_part = (int)off;
     off += align16(std::max((size_t)max_items * 64, (size_t)RMAX * (D + 2) * 4));

@@ -260,6 +260,45 @@ def test_trunk_matches_per_op_long_context():
     print(f"  worst logits max-abs-rel {worst:.2e}", flush=True)
 
 
+def test_control_wave_item_same_bits(monkeypatch):
+    """2049-2304 positions on the Llama-3-8B shape (32 key ranges per kv head): 9
+    items per attention unit for 8 worker waves, so the control wave computes each
+    unit's last item from its own LDS area (loaded while q|k|v is computed).  The
+    item states merge in item order, so the steps are bit for bit those of a plan in
+    which the workers take every item (SC_TRUNK_CONTROL_ITEM=0 at plan creation), and
+    within the tolerance of the per-op path."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU visible")
+    m = build(LLAMA8B_2L, 4, 2304, seed=13)
+    print("trunk control-wave item: Llama-3-8B shape, 2 layers, prompt 2060 vs per-op", flush=True)
+    worst = compare_paths(m, 2060, steps=3, capacity=2304)
+    print(f"  worst logits max-abs-rel {worst:.2e}", flush=True)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(6)
+    ids = torch.randint(0, m.vocab_size, (1, 2060), generator=gen, device="cuda")
+    ca = m.new_cache(1, 2304)
+    logits, _ = asyncio.run(m.forward(ids, past_key_values=ca, use_cache=True, last_only=True))
+    cb = clone_cache(m, ca)
+    outs = []
+    for c, env in ((ca, None), (cb, "0")):
+        print(f"trunk control-wave item: SC_TRUNK_CONTROL_ITEM={env}", flush=True)
+        if env is None:
+            monkeypatch.delenv("SC_TRUNK_CONTROL_ITEM", raising=False)
+        else:
+            monkeypatch.setenv("SC_TRUNK_CONTROL_ITEM", env)
+        t = torch.zeros((1, 8), dtype=torch.int32, device="cuda")
+        d = DecodeGraph(m, c, t, use_graph=False, fused_trunk=True)
+        assert d.bufs.plan is not None
+        _lib.argmax(logits.reshape(1, -1), ids=d.bufs.ids.view(-1), tokens=t, step=c.counters[1:])
+        _lib.add_i32(c.counters[1:], 1, n=1)
+        d.run(5)
+        torch.cuda.synchronize()
+        assert d.bufs.plan.status() == 0
+        outs.append((t.clone(), c.k.clone(), c.vt.clone(), d.logits.clone()))
+    for x, y in zip(outs[0], outs[1]):
+        assert torch.equal(x, y)
+
+
 def test_trunk_repeatable_long_context():
     """Two fused runs from the same cache give bit-identical caches and tokens, also
     when the attention items of a unit land on different waves from run to run."""
