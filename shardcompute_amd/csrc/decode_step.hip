@@ -67,6 +67,9 @@ constexpr unsigned long long TIMEOUT_TICKS = 20000000ull;   // 200 ms of the 100
 // template parameters of the kernel: (128, 4) for the Llama-3 shapes, (64, 8) for
 // TinyLlama's
 
+// Projection tiles per workgroup and op whose outputs the control wave publishes as
+// they complete (ops with more publish at the op boundary)
+constexpr int MAX_TILES = 64;
 constexpr int NT = 6;                       // ops per layer, in this order:
 enum OpKind { K_QKV = 0, K_ATTN = 1, K_MERGE = 2, K_O = 3, K_GU = 4, K_DOWN = 5 };
 enum OpFlags { F_NORM = 1, F_SWIGLU = 2, F_RESID = 4, F_ROW8 = 8 };
@@ -242,6 +245,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     __shared__ int s_pre[NT + 1];           // this workgroup's items per layer, prefix over op kinds
     __shared__ int s_total;
     __shared__ int s_abort;                 // a poll gave up: every wave skips the remaining work
+    __shared__ int s_tile[MAX_TILES];       // per projection tile of the current op: chunks computed
     __shared__ float s_red[NORM_THREADS / 64];
 
     const int tid = threadIdx.x;
@@ -489,6 +493,49 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     };
     auto kind_of = [&](int j) -> int { return j == 0 ? -1 : (j - 1) % NT; };
 
+    // Control wave: publish projection op kp's tiles [t0, t1) of layer lp_ (each tile's
+    // K-chunk partials summed in chunk order from part; SwiGLU, residual add and the
+    // last layer's plain copy applied).
+    auto publish_tiles = [&](int kp, int lp_, uint32_t ep, int t0, int t1) __attribute__((always_inline)) {
+        const GemvDesc &o = sgd[gemv_index(kp)];
+        const int cpt = o.cpt;
+        uint2 *dst = o.out;
+        uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
+        if (o.flags & F_SWIGLU) {
+            // tile tl: gate columns 8 (tb + tl) + c, c < 8; 4 words per tile
+            for (int wdx = 4 * t0 + lane; wdx < t1 * 4; wdx += 64) {
+                const int tl = wdx >> 2, c = 2 * (wdx & 3);
+                const float *pp = part + (size_t)tl * cpt * 16;
+                float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
+                chunk_sums(pp + c, cpt, g0, g1);
+                chunk_sums(pp + 8 + c, cpt, u0, u1);
+                const uint32_t o0 = f2bf(silu_mul_f(bf2f(f2bf(g0)), bf2f(f2bf(u0))));
+                const uint32_t o1 = f2bf(silu_mul_f(bf2f(f2bf(g1)), bf2f(f2bf(u1))));
+                ll_store(dst + (((o.rb >> 4) + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
+            }
+        } else {
+            const uint32_t *hw = reinterpret_cast<const uint32_t *>(hbuf);
+            const bool resid = o.flags & F_RESID;
+            for (int wdx = 8 * t0 + lane; wdx < t1 * 8; wdx += 64) {
+                const int tl = wdx >> 3, c = 2 * (wdx & 7);
+                const int n = o.rb + tl * 16 + c;
+                if (n >= o.re) continue;                    // a half tile's duplicate rows
+                const float *pp = part + (size_t)tl * cpt * 16;
+                float v0 = 0.f, v1 = 0.f;
+                chunk_sums(pp + c, cpt, v0, v1);
+                uint32_t o0 = f2bf(v0), o1 = f2bf(v1);
+                if (resid) {
+                    const uint32_t hv = hw[n / 2];
+                    o0 = f2bf(add_rn(bf2f(hv & 0xFFFFu), bf2f(o0)));
+                    o1 = f2bf(add_rn(bf2f(hv >> 16), bf2f(o1)));
+                }
+                ll_store(dst + n / 2, o0 | (o1 << 16), ep);
+                if (plain) *reinterpret_cast<uint32_t *>(plain + n) = o0 | (o1 << 16);
+            }
+        }
+    };
+    int early_done = -1;                    // (control wave) the op whose tiles are all published
+
     // is_ctl: std::true_type in the control wave's copy, std::false_type in the
     // workers' (the control wave's polls then cost the workers no registers)
     auto boundary = [&](int jj, auto is_ctl) __attribute__((always_inline)) {
@@ -568,43 +615,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                         reinterpret_cast<const uint32_t *>(a.embed + (inr ? local : 0) * (size_t)a.hidden);
                     for (int w = wg * per + lane; w < min(words, (wg + 1) * per); w += 64)
                         ll_store(a.buf[B_H] + w, inr ? row[w] : 0u, ep);
-                } else {
-                    const GemvDesc &o = sgd[gemv_index(kp)];
-                    const int ntl = o.ntl, cpt = o.cpt;
-                    uint2 *dst = o.out;
-                    uint16_t *plain = (kp == K_DOWN && lp_ == a.L - 1) ? a.h_out : nullptr;
-                    if (o.flags & F_SWIGLU) {
-                        // tile tl: gate columns 8 (tb + tl) + c, c < 8; 4 words per tile
-                        for (int wdx = lane; wdx < ntl * 4; wdx += 64) {
-                            const int tl = wdx >> 2, c = 2 * (wdx & 3);
-                            const float *pp = part + (size_t)tl * cpt * 16;
-                            float g0 = 0.f, g1 = 0.f, u0 = 0.f, u1 = 0.f;
-                            chunk_sums(pp + c, cpt, g0, g1);
-                            chunk_sums(pp + 8 + c, cpt, u0, u1);
-                            const uint32_t o0 = f2bf(silu_mul_f(bf2f(f2bf(g0)), bf2f(f2bf(u0))));
-                            const uint32_t o1 = f2bf(silu_mul_f(bf2f(f2bf(g1)), bf2f(f2bf(u1))));
-                            ll_store(dst + (((o.rb >> 4) + tl) * 8 + c) / 2, o0 | (o1 << 16), ep);
-                        }
-                    } else {
-                        const uint32_t *hw = reinterpret_cast<const uint32_t *>(hbuf);
-                        const bool resid = o.flags & F_RESID;
-                        for (int wdx = lane; wdx < ntl * 8; wdx += 64) {
-                            const int tl = wdx >> 3, c = 2 * (wdx & 7);
-                            const int n = o.rb + tl * 16 + c;
-                            if (n >= o.re) continue;                    // a half tile's duplicate rows
-                            const float *pp = part + (size_t)tl * cpt * 16;
-                            float v0 = 0.f, v1 = 0.f;
-                            chunk_sums(pp + c, cpt, v0, v1);
-                            uint32_t o0 = f2bf(v0), o1 = f2bf(v1);
-                            if (resid) {
-                                const uint32_t hv = hw[n / 2];
-                                o0 = f2bf(add_rn(bf2f(hv & 0xFFFFu), bf2f(o0)));
-                                o1 = f2bf(add_rn(bf2f(hv >> 16), bf2f(o1)));
-                            }
-                            ll_store(dst + n / 2, o0 | (o1 << 16), ep);
-                            if (plain) *reinterpret_cast<uint32_t *>(plain + n) = o0 | (o1 << 16);
-                        }
-                    }
+                } else if (jp != early_done) {
+                    publish_tiles(kp, lp_, ep, 0, sgd[gemv_index(kp)].ntl);
                 }
             }
         }
@@ -618,6 +630,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         const int l = jj == 0 ? -1 : (jj - 1) / NT;
         const uint32_t ep_in = epoch(jj - 1);                        // every op reads the previous op's output
         const bool is_gemv = k == K_QKV || k == K_O || k == K_GU || k == K_DOWN;
+        if (ctl && is_gemv)
+            for (int t = lane; t < MAX_TILES; t += 64) s_tile[t] = 0;   // the workers count after B3
         const GemvDesc &o = sgd[is_gemv ? gemv_index(k) : 0];
         const int W = o.K >> 3;
         const bool wide = is_gemv && !(o.flags & F_NORM) && W > 512;     // every wave polls
@@ -821,7 +835,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     for (int k = 0; k < NT; ++k) pre[k] = s_pre[k];
     const unsigned ipl_magic = ipl > 1 ? (unsigned)((0x100000000ULL + (unsigned)ipl - 1) / (unsigned)ipl) : 0u;
     struct ItemLoc {
-        int l, k, i, ch;
+        int l, k, i, ch, tl;
     };
     // DMA of attention item i of this workgroup's unit (layer lp) to LDS dst
     auto dma_attn = [&](const LayerPtrs &lp, int i, uint32_t dst) __attribute__((always_inline)) {
@@ -864,6 +878,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         w.k = kind;
         w.i = r - base_k;
         w.ch = 0;
+        w.tl = 0;
         const LayerPtrs &lp = slp[w.l];
         const uint32_t d1 = dst + 1024, d2 = dst + 2048, d3 = dst + 3072, d4 = dst + 4096;
         if (w.k != K_ATTN) {
@@ -873,6 +888,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             const int tl = cpt == 1 ? w.i : (int)__umulhi((unsigned)w.i, o.cpt_magic);
             const int ch = w.i - tl * cpt;
             w.ch = ch;
+            w.tl = tl;
             const int n0 = o.rb + tl * 16;             // this workgroup's rows [o.rb, o.re)
             const int rlast = o.re - 1;
             const uint32_t row_bytes = (uint32_t)o.K * BITS / 8;        // every weight matrix < 4 GB
@@ -1043,6 +1059,34 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     attn_compute(ni_unit - 1, own);
                 }
             }
+            // a projection's tiles published as the workers complete them (all of a tile's
+            // K chunks counted), so that the op boundary finds them out already
+            const int kj = jj >= 1 && jj < nops ? kind_of(jj) : -1;
+            if ((kj == K_QKV || kj == K_O || kj == K_GU || kj == K_DOWN) && !s_abort) {
+                const GemvDesc &o = sgd[gemv_index(kj)];
+                if (o.ntl <= MAX_TILES) {
+                    const uint32_t ep = epoch(jj);
+                    const int lj = (jj - 1) / NT;
+                    int t0 = 0;
+                    for (int it = 0; t0 < o.ntl; ++it) {
+                        int t1 = t0;
+                        while (t1 < o.ntl &&
+                               __hip_atomic_load(&s_tile[t1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+                                   o.cpt)
+                            ++t1;
+                        if (t1 > t0) {
+                            __builtin_amdgcn_s_setprio(3);
+                            publish_tiles(kj, lj, ep, t0, t1);
+                            __builtin_amdgcn_s_setprio(0);
+                            t0 = t1;
+                            continue;
+                        }
+                        if (s_abort || ((it & 255) == 255 && expired())) break;
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    if (t0 == o.ntl) early_done = jj;
+                }
+            }
         }
         wait_vm<0>();                                   // no DMA may land after the workgroup ends
         if (lane == 0 && s_abort) atomicOr(a.status, 2u);
@@ -1060,7 +1104,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         const uint32_t ring_lds = (uint32_t)(uintptr_t)ring;
 
         // per ring slot: op index, op kind, item of the op, and (projections) its K chunk
-        int sj[TRING], sk[TRING], si[TRING], sch[TRING];
+        // and tile
+        int sj[TRING], sk[TRING], si[TRING], sch[TRING], stl[TRING];
         // DMA of item g into ring slot `slot`
         auto issue = [&](int g, int slot) {
             const ItemLoc w = dma_item(min(g, total - 1), ring_lds + slot * SLOT);
@@ -1068,6 +1113,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             sk[slot] = w.k;
             si[slot] = w.i;
             sch[slot] = w.ch;
+            stl[slot] = w.tl;
         };
 
         // ---- projection item (the math of qgemv_m1_kernel)
@@ -1174,6 +1220,11 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             } else {
                                 wait_vm<DMA_PER_ITEM * (TRING - 1)>();
                                 compute(s);
+                                // the item's partials are in LDS: count it for its tile (the
+                                // release orders this wave's LDS writes before the count)
+                                if (sk[s] != K_ATTN && stl[s] < MAX_TILES && lane == 0)
+                                    __hip_atomic_fetch_add(&s_tile[stl[s]], 1, __ATOMIC_RELEASE,
+                                                           __HIP_MEMORY_SCOPE_WORKGROUP);
                             }
                         }
                     }
@@ -1320,7 +1371,7 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
     a.o_lp = (int)off; off += (size_t)L * sizeof(LayerPtrs);
     a.lds_bytes = (int)off;
     const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
-    if (off + 128 > (size_t)lds_cap)
+    if (off + 512 > (size_t)lds_cap)                 // + the kernel's static LDS (under 512 bytes)
         return set_error(SC_EUNSUPPORTED, "decode_plan: needs %zu bytes of LDS (limit %d)", off, lds_cap);
 
     // device memory: layer table, exchange buffers, epoch base, status
