@@ -556,8 +556,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
             if (kp == K_ATTN) {
                 if (au.valid) {
                     // merge the items' (m, l, O) per head, in item order (the same sums
-                    // whichever wave computed which item), into part: [R][D + 2] = O
-                    // (unnormalised), m, l.  Each value's thread takes the head's maximum M
+                    // whichever wave computed which item), into the unit's [R][D + 2]
+                    // words: O (unnormalised), m, l.  Each value's thread takes the head's maximum M
                     // over the items and weighs item i by exp2(m_i - M), one fma per item:
                     // one pass (the maxima are broadcast reads), no barrier inside.
                     const int ni = au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
@@ -597,11 +597,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                                 acc = fmaf((mw == -INFINITY) ? 0.f : exp2f(mw - M), src[w * AST], acc);
                             }
                         }
-                        part[t] = acc;
+                        ll_store(dst + t, __float_as_uint(acc), ep);    // each thread publishes its value
                     }
-                    __syncthreads();
-                    if (ctl)
-                        for (int t = lane; t < a.R * (D + 2); t += 64) ll_store(dst + t, __float_as_uint(part[t]), ep);
                 }
             } else if (kp != K_MERGE && ctl) {
                 if (jp == 0) {
@@ -1362,9 +1359,9 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
         const char *ev = getenv("SC_TRUNK_CONTROL_ITEM");
         if (ev && ev[0] == '0') a.o_spare = -1;
     }
-    // projection partials, or the attention merge [RMAX][D + 2]
+    // projection partials: 16 floats per item
     a.o_part = (int)off;
-    off += align16(std::max((size_t)max_items * 64, (size_t)RMAX * (D + 2) * 4));
+    off += align16((size_t)max_items * 64);
     a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
     a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
     a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
