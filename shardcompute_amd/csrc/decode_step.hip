@@ -557,45 +557,33 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 if (au.valid) {
                     // merge the items' (m, l, O) per head, in item order (the same sums
                     // whichever wave computed which item), into the unit's [R][D + 2]
-                    // words: O (unnormalised), m, l.  Each value's thread takes the head's maximum M
-                    // over the items and weighs item i by exp2(m_i - M), one fma per item:
-                    // one pass (the maxima are broadcast reads), no barrier inside.
-                    const int ni = au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
+                    // words: O (unnormalised), m, l.  The control wave has put each
+                    // item's weight exp2(m_i - M) per head in part (fac[h][i], the head's
+                    // maximum M after them) as the items completed; one fma per item and
+                    // value here.
+                    const int ni = ni_unit;
                     uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
+                    const float *fac = part, *mh = part + a.R * ni;
                     for (int t = tid; t < a.R * (D + 2); t += THREADS) {
                         const int h = t / (D + 2), x = t - h * (D + 2);
-                        const float *mrow = ast + h * (D + 4) + D;
-                        float M = -INFINITY;
-                        int v = 0;
-                        for (; v + 4 <= ni; v += 4) {              // reads 4 at a time
-                            float m4[4];
-#pragma unroll
-                            for (int k = 0; k < 4; ++k) m4[k] = mrow[(v + k) * AST];
-#pragma unroll
-                            for (int k = 0; k < 4; ++k) M = fmaxf(M, m4[k]);
-                        }
-                        for (; v < ni; ++v) M = fmaxf(M, mrow[v * AST]);
                         float acc = 0.f;
                         if (x == D) {
-                            acc = ni > 0 ? M : -INFINITY;
+                            acc = ni > 0 ? mh[h] : -INFINITY;
                         } else {
                             const float *src = ast + h * (D + 4) + x;          // x = D + 1: l
+                            const float *fh = fac + h * ni;
                             int w = 0;
                             for (; w + 4 <= ni; w += 4) {          // reads 4 items at a time
-                                float mw[4], o[4];
+                                float f[4], o[4];
 #pragma unroll
                                 for (int k = 0; k < 4; ++k) {
-                                    mw[k] = mrow[(w + k) * AST];
+                                    f[k] = fh[w + k];
                                     o[k] = src[(w + k) * AST];
                                 }
 #pragma unroll
-                                for (int k = 0; k < 4; ++k)
-                                    acc = fmaf((mw[k] == -INFINITY) ? 0.f : exp2f(mw[k] - M), o[k], acc);
+                                for (int k = 0; k < 4; ++k) acc = fmaf(f[k], o[k], acc);
                             }
-                            for (; w < ni; ++w) {
-                                const float mw = mrow[w * AST];
-                                acc = fmaf((mw == -INFINITY) ? 0.f : exp2f(mw - M), src[w * AST], acc);
-                            }
+                            for (; w < ni; ++w) acc = fmaf(fh[w], src[w * AST], acc);
                         }
                         ll_store(dst + t, __float_as_uint(acc), ep);    // each thread publishes its value
                     }
@@ -627,7 +615,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
         const int l = jj == 0 ? -1 : (jj - 1) / NT;
         const uint32_t ep_in = epoch(jj - 1);                        // every op reads the previous op's output
         const bool is_gemv = k == K_QKV || k == K_O || k == K_GU || k == K_DOWN;
-        if (ctl && is_gemv)
+        if (ctl && (is_gemv || k == K_ATTN))
             for (int t = lane; t < MAX_TILES; t += 64) s_tile[t] = 0;   // the workers count after B3
         const GemvDesc &o = sgd[is_gemv ? gemv_index(k) : 0];
         const int W = o.K >> 3;
@@ -1056,9 +1044,35 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     attn_compute(ni_unit - 1, own);
                 }
             }
+            const int kj = jj >= 1 && jj < nops ? kind_of(jj) : -1;
+            // the attention items' merge weights, once the workers' items are counted
+            if (kj == K_ATTN && ni_unit > 0 && !s_abort) {
+                const int nw = ni_unit - (ctl_item ? 1 : 0);
+                bool ready = true;
+                for (int it = 0;
+                     __hip_atomic_load(&s_tile[0], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < nw; ++it) {
+                    if (s_abort || ((it & 255) == 255 && expired())) {
+                        ready = false;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                if (ready) {
+                    const int ni = ni_unit;
+                    float *fac = part, *mh = part + a.R * ni;
+                    for (int t = lane; t < a.R * ni; t += 64) {
+                        const int h = t / ni, w = t - h * ni;
+                        const float *mrow = ast + h * (D + 4) + D;
+                        float M = -INFINITY;
+                        for (int v = 0; v < ni; ++v) M = fmaxf(M, mrow[v * AST]);
+                        const float mw = mrow[w * AST];
+                        fac[t] = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+                        if (w == 0) mh[h] = M;
+                    }
+                }
+            }
             // a projection's tiles published as the workers complete them (all of a tile's
             // K chunks counted), so that the op boundary finds them out already
-            const int kj = jj >= 1 && jj < nops ? kind_of(jj) : -1;
             if ((kj == K_QKV || kj == K_O || kj == K_GU || kj == K_DOWN) && !s_abort) {
                 const GemvDesc &o = sgd[gemv_index(kj)];
                 if (o.ntl <= MAX_TILES) {
@@ -1217,9 +1231,10 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             } else {
                                 wait_vm<DMA_PER_ITEM * (TRING - 1)>();
                                 compute(s);
-                                // the item's partials are in LDS: count it for its tile (the
-                                // release orders this wave's LDS writes before the count)
-                                if (sk[s] != K_ATTN && stl[s] < MAX_TILES && lane == 0)
+                                // the item's partials (or attention state) are in LDS: count
+                                // it for its tile (attention: tile 0; the release orders this
+                                // wave's LDS writes before the count)
+                                if (stl[s] < MAX_TILES && lane == 0)
                                     __hip_atomic_fetch_add(&s_tile[stl[s]], 1, __ATOMIC_RELEASE,
                                                            __HIP_MEMORY_SCOPE_WORKGROUP);
                             }
@@ -1359,9 +1374,10 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
         const char *ev = getenv("SC_TRUNK_CONTROL_ITEM");
         if (ev && ev[0] == '0') a.o_spare = -1;
     }
-    // projection partials: 16 floats per item
+    // projection partials (16 floats per item), or the attention items' merge weights
+    // [R][n_items] and maxima [R]
     a.o_part = (int)off;
-    off += align16((size_t)max_items * 64);
+    off += align16(std::max((size_t)max_items * 64, ((size_t)RMAX * n_items + RMAX) * 4));
     a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
     a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
     a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
