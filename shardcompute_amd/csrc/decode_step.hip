@@ -1092,8 +1092,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             t0 = t1;
                             continue;
                         }
+                        // polled without a sleep (measured: TinyLlama 0.4 % faster, 8B the same)
                         if (s_abort || ((it & 255) == 255 && expired())) break;
-                        __builtin_amdgcn_s_sleep(1);
                     }
                     if (t0 == o.ntl) early_done = jj;
                 }
