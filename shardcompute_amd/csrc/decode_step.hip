@@ -113,6 +113,7 @@ struct Args {
     // LDS layout (byte offsets into dynamic shared memory)
     int o_xl, o_xzero, o_xs, o_part, o_hbuf, o_qkv, o_gd, o_lp, lds_bytes;
     int o_spare;            // the control wave's attention item area (in x's), or -1
+    int single_max;         // contexts up to this length use one key range per kv head
     uint32_t *trace;          // null, or [P][nops][4] real-time stamps of the last launch
 };
 
@@ -266,7 +267,14 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
 
     const int pos = a.counters[0];
     const int T = pos + 1;                  // keys after the append
-    int kps = (T + a.NR - 1) / a.NR;
+    // Keys per attention unit: the context split over NR ranges per kv head, or, for
+    // contexts up to single_max, one range holding every key: its unit then finishes
+    // the attention itself and the merge op has nothing to do (its exchange and
+    // boundary cost more than a second round of items).
+    // (compiled for head_dim 64 only: in the 128 instantiation the extra code cost the
+    // Llama-3-8B step 0.8 %, and its contexts above 2048 positions never use it)
+    const bool single = D == 64 && T <= a.single_max;
+    int kps = single ? T : (T + a.NR - 1) / a.NR;
     kps = (kps + 7) & ~7;
     const uint32_t base = a.epoch_base[0];
     const AttnUnit au = attn_unit(a, wg, T, kps);
@@ -278,7 +286,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     // (head_dim 128 only: at 64 the x area rarely has room beside the states, and the
     // code in the control wave's path costs the other instantiation's boundaries
     // registers: TinyLlama 0.741 -> 0.746 ms a step with it compiled in)
-    const bool ctl_item = D == 128 && a.o_spare >= 0 && ni_unit > WORKERS;
+    const bool ctl_item = D == 128 && !single && a.o_spare >= 0 && ni_unit > WORKERS;
 
     // ---- set-up by the control wave: shapes and layer pointers into LDS, this
     // workgroup's items per op kind; then the one workgroup-wide barrier
@@ -564,6 +572,26 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                     const int ni = ni_unit;
                     uint2 *dst = a.buf[B_PART] + (size_t)(au.kvh * a.NR + au.r) * a.R * (D + 2);
                     const float *fac = part, *mh = part + a.R * ni;
+                    if (single) {
+                        // the kv head's one range: the attention output itself, O / l in
+                        // bf16 as the merge computes it for a single range (weight 1, the
+                        // range's l), published as the merge op's output
+                        if (au.r == 0) {
+                            for (int t = tid; t < a.R * (D / 2); t += THREADS) {
+                                const int h = t / (D / 2), x = 2 * (t - h * (D / 2));
+                                const float *src = ast + h * (D + 4) + x, *fh = fac + h * ni;
+                                float o0 = 0.f, o1 = 0.f, l = 0.f;
+                                for (int w = 0; w < ni; ++w) {
+                                    o0 = fmaf(fh[w], src[w * AST], o0);
+                                    o1 = fmaf(fh[w], src[w * AST + 1], o1);
+                                    l = fmaf(fh[w], src[w * AST + (D + 1 - x)], l);
+                                }
+                                const float inv = 1.f / l;
+                                ll_store(a.buf[B_ATT] + ((size_t)(au.kvh * a.R + h) * D + x) / 2,
+                                         pack_bf16x2(o0 * inv, o1 * inv), epoch(jp + 1));
+                            }
+                        }
+                    } else
                     for (int t = tid; t < a.R * (D + 2); t += THREADS) {
                         const int h = t / (D + 2), x = t - h * (D + 2);
                         float acc = 0.f;
@@ -690,7 +718,7 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                 // (m, l) and its C values of O, then the ranges merge across lanes
                 const int C = a.C_merge;
                 const int c0 = wg * C;
-                if (c0 < a.H * D) {
+                if (!single && c0 < a.H * D) {
                     const int hq = c0 / D, d0 = c0 - hq * D;
                     const int kvh = hq / a.R, hr = hq - kvh * a.R;
                     const uint2 *src = a.buf[B_PART];
@@ -1355,37 +1383,65 @@ int decode_plan_create(const sc_decode_model *m, const sc_decode_layer *layers, 
         const int tiles = (g.flags & F_ROW8) ? (((g.N + 7) / 8 + P - 1) / P + 1) / 2 : (g.T + P - 1) / P;
         max_items = std::max(max_items, tiles * g.cpt);
     }
-    size_t off = (size_t)WORKERS * TRING * SLOT;
-    // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 2) floats
+    // attention item states: ceil(keys per unit / 8) blocks of RMAX (D + 4) floats
     const int kps_max = ((m->T_cap + NR - 1) / NR + 7) & ~7;
     const int n_items = kps_max / 8;            // attention items per unit at most
-    const size_t ast_bytes = (size_t)n_items * RMAX * (D + 4) * 4;
-    a.o_xl = (int)off; off += align16(std::max((size_t)Kmax * 2, ast_bytes));
-    a.o_xzero = (int)off; off += 1024;
-    a.o_xs = (int)off; off += align16((size_t)(Kmax / 64) * 4);
+    const size_t item_state = (size_t)RMAX * (D + 4) * 4;
+    const size_t ast_bytes = (size_t)n_items * item_state;
+    const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
+    // the layout for an x area of xarea bytes (which the attention states overlay) and
+    // merge weights for up to fac_items items per unit; returns the bytes used
+    auto layout = [&](size_t xarea, int fac_items) -> size_t {
+        size_t o = (size_t)WORKERS * TRING * SLOT;
+        a.o_xl = (int)o; o += xarea;
+        a.o_xzero = (int)o; o += 1024;
+        a.o_xs = (int)o; o += align16((size_t)(Kmax / 64) * 4);
+        // projection partials (16 floats per item), or the attention items' merge
+        // weights [R][items] and maxima [R]
+        a.o_part = (int)o;
+        o += align16(std::max((size_t)max_items * 64, ((size_t)RMAX * fac_items + RMAX) * 4));
+        a.o_hbuf = (int)o; o += align16((size_t)hid * 2);
+        a.o_qkv = (int)o; o += align16((size_t)(RMAX + 2) * D * 2);
+        a.o_gd = (int)o; o += align16(4 * sizeof(GemvDesc));
+        a.o_lp = (int)o; o += (size_t)L * sizeof(LayerPtrs);
+        return o;
+    };
+    size_t xarea = align16(std::max((size_t)Kmax * 2, ast_bytes));
+    size_t off = layout(xarea, n_items);
+    if (off + 512 > (size_t)lds_cap)                 // + the kernel's static LDS (under 512 bytes)
+        return set_error(SC_EUNSUPPORTED, "decode_plan: needs %zu bytes of LDS (limit %d)", off, lds_cap);
+    // One key range per kv head for contexts up to 8 x single_items positions (at most
+    // 8 items, one round of the workers: with 16, TinyLlama was 0.8 % slower than with
+    // the ranges and their merge), the x area grown into the LDS left over to hold
+    // their states.  head_dim 64 only.  SC_TRUNK_SINGLE_RANGE=0 at plan creation turns
+    // it off.
+    int single_items = 0;
+    {
+        const char *ev = getenv("SC_TRUNK_SINGLE_RANGE");
+        if (D == 64 && !(ev && ev[0] == '0')) {
+            for (int si = 8; si >= 1; --si) {
+                const size_t xa = align16(std::max(xarea, (size_t)si * item_state));
+                if (layout(xa, std::max(n_items, si)) + 512 <= (size_t)lds_cap) {
+                    single_items = si;
+                    xarea = xa;
+                    break;
+                }
+            }
+        }
+        off = layout(xarea, std::max(n_items, single_items));
+    }
+    a.single_max = 8 * single_items;
     // the control wave's attention item (one ring slot), in the x area past q|k|v's
     // input and the attention states, when it fits there.  SC_TRUNK_CONTROL_ITEM=0 in
     // the environment at plan creation leaves every item to the workers (the results
     // are the same bits: the states merge in item order whoever computed them).
     {
-        const size_t xarea = align16(std::max((size_t)Kmax * 2, ast_bytes));
         const size_t rel = align16(std::max(ast_bytes, (size_t)hid * 2));
         a.o_spare = rel + SLOT <= xarea ? (int)(a.o_xl + rel) : -1;
         const char *ev = getenv("SC_TRUNK_CONTROL_ITEM");
         if (ev && ev[0] == '0') a.o_spare = -1;
     }
-    // projection partials (16 floats per item), or the attention items' merge weights
-    // [R][n_items] and maxima [R]
-    a.o_part = (int)off;
-    off += align16(std::max((size_t)max_items * 64, ((size_t)RMAX * n_items + RMAX) * 4));
-    a.o_hbuf = (int)off; off += align16((size_t)hid * 2);
-    a.o_qkv = (int)off; off += align16((size_t)(RMAX + 2) * D * 2);
-    a.o_gd = (int)off; off += align16(4 * sizeof(GemvDesc));
-    a.o_lp = (int)off; off += (size_t)L * sizeof(LayerPtrs);
     a.lds_bytes = (int)off;
-    const int lds_cap = di.max_lds_per_block < 160 * 1024 ? di.max_lds_per_block : 160 * 1024;
-    if (off + 512 > (size_t)lds_cap)                 // + the kernel's static LDS (under 512 bytes)
-        return set_error(SC_EUNSUPPORTED, "decode_plan: needs %zu bytes of LDS (limit %d)", off, lds_cap);
 
     // device memory: layer table, exchange buffers, epoch base, status
     const size_t nb_h = (size_t)hid / 2, nb_qkv = (size_t)qkvN / 2, nb_part = (size_t)Hkv * NR * R * (D + 2),
