@@ -16,9 +16,14 @@
 // Roles inside a workgroup: 8 worker waves claim 4 KB items (16 weight rows x 256 B
 // plus scales/biases, or 8 cached keys with their values) from one counter spanning
 // all ops of the step, DMA them into their ring and compute them; one control wave
-// polls each op's input and publishes each op's output.  At each op boundary all
-// nine waves meet (LDS barriers only) and share the staging work (norm, operand
-// permutation, merging the workers' attention states).  Workgroups exchange activations through "LL" words: 8-byte (data, epoch)
+// polls each op's input and publishes each op's output.  While the workers compute
+// an op's items the control wave publishes each projection tile as soon as its K
+// chunks are counted, computes the attention items' merge weights once they are in,
+// and (9 items for 8 workers) computes a unit's last attention item itself.  At each
+// op boundary all nine waves meet (LDS barriers only) and share the staging work
+// (norm, operand permutation, merging the workers' attention states).
+//
+// Workgroups exchange activations through "LL" words: 8-byte (data, epoch)
 // pairs written with one agent-coherent store, so a reader that sees the epoch of
 // the current op and launch also sees the data (no flags, no fences, no grid
 // barrier).  Each op kind has its own exchange buffer; a buffer is rewritten one
