@@ -707,8 +707,12 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                         }
                         // the unit holding the new position appends it to the cache
                         if (au.lo <= T - 1 && T - 1 < au.hi) {
-                            uint16_t *kd = slp[l].kc + ((size_t)au.kvh * a.T_cap + (T - 1)) * D;
-                            uint16_t *vd = slp[l].vt + (size_t)au.kvh * D * a.T_cap + (T - 1);
+                            // global stores (the pointers come from LDS: as FLAT stores they
+                            // would also hold up this wave's LDS waits until they complete,
+                            // and the value column's 128 two-byte stores take long)
+                            typedef __attribute__((address_space(1))) uint16_t g_u16;
+                            g_u16 *kd = (g_u16 *)(slp[l].kc + ((size_t)au.kvh * a.T_cap + (T - 1)) * D);
+                            g_u16 *vd = (g_u16 *)(slp[l].vt + (size_t)au.kvh * D * a.T_cap + (T - 1));
                             const uint16_t *kr = qkv_l + RMAX * D, *vr = qkv_l + RMAX * D + D;
 #pragma unroll
                             for (int i = lane; i < D; i += 64) {
