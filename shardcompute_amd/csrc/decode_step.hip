@@ -288,9 +288,8 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
     // the items are computed, takes the last one: loaded into its own LDS area while
     // q|k|v is computed, so the op needs one round of items instead of two.
     const int ni_unit = au.valid && au.hi > au.lo ? (au.hi - au.lo + 7) >> 3 : 0;
-    // (head_dim 128 only: at 64 the x area rarely has room beside the states, and the
-    // code in the control wave's path costs the other instantiation's boundaries
-    // registers: TinyLlama 0.741 -> 0.746 ms a step with it compiled in)
+    // (head_dim 128 only: at 64, with 8 query heads per kv head, the states of 9 items
+    // fill the x area of TinyLlama-sized layers, so the item area would not fit)
     const bool ctl_item = D == 128 && !single && a.o_spare >= 0 && ni_unit > WORKERS;
 
     // ---- set-up by the control wave: shapes and layer pointers into LDS, this
