@@ -1128,8 +1128,13 @@ __global__ void __launch_bounds__(THREADS) decode_step_kernel(Args a) {
                             t0 = t1;
                             continue;
                         }
-                        // polled without a sleep (measured: TinyLlama 0.4 % faster, 8B the same)
-                        if (s_abort || ((it & 255) == 255 && expired())) break;
+                        // polled without a sleep (measured: TinyLlama 0.4 % faster, 8B the same);
+                        // a launch that gives up here records it and stops every wave
+                        if (s_abort) break;
+                        if ((it & 255) == 255 && timed_out()) {
+                            if (lane == 0) s_abort = 1;
+                            break;
+                        }
                     }
                     if (t0 == o.ntl) early_done = jj;
                 }
